@@ -1,0 +1,215 @@
+"""Benchmark: fused Flash-GMM EM iterations per second on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--config 2] [--all]
+                    [--variant auto|valu|mfma] [--no-cpu-baseline]
+
+A step is one fused EM iteration (precompute -> Pass 1 -> Pass 2 ->
+reduction/M-step) over the configuration's full synthetic data set, which is
+resident in HBM before timing starts.  The timed region runs ``steps``
+iterations back to back on the device (parameters fed forward on the device,
+no host synchronisation inside), bracketed by ``torch.cuda.synchronize()``.
+Pass 2's launch durations are measured live with HIP events on the launch
+stream (``fgmm_profile_*``) and give the roofline figure.
+
+Default workload: configuration 2 (N=65536, K=256, d=128, fp32), the metric's
+headline shape.  ``--all`` adds one JSON line per configuration after the
+headline line.  The CPU baseline is the reference's own C++/OpenMP standard
+E+M (``flash_gmm_cpu.cpp`` standard_e_step + standard_m_step) compiled into
+``oracle/_ref``, timed on a bounded sample of the same workload on rank 0;
+if that build is absent, this repository's fp32 restatement of it
+(``oracle/fgmm_oracle.c``) is timed instead and labelled "port".
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+from flashgmm_amd.configs import CONFIGS, make_problem  # noqa: E402
+
+HBM_PEAK = 8.0e12        # B/s, MI355X
+FP32_PEAK = 157.3e12     # FLOP/s, MI355X dense fp32 (vector = matrix)
+FP64_PEAK = 78.6e12      # FLOP/s, MI355X dense fp64 (vector = matrix)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--all", action="store_true", help="also report every configuration")
+    ap.add_argument("--variant", default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="target CPU time for the baseline sample")
+    return ap.parse_args()
+
+
+def pass2_flops(cfg) -> float:
+    # gamma recompute (4 flops per (n,k,j)) + gamma^T [X, X^2] (4 per (n,k,j))
+    return 8.0 * cfg.N * cfg.K * cfg.d
+
+
+def pass2_peak() -> float:
+    # Pass 2's two contractions run at different precisions: the distance on
+    # fp64 matrix cores, the statistics on fp32 matrix cores.  The binding
+    # peak for its 8 flops per (n,k,j) is the time-weighted mix.
+    return 8.0 / (4.0 / FP64_PEAK + 4.0 / FP32_PEAK)
+
+
+def run_gpu(cid, steps, warmup, variant):
+    import torch
+    from flashgmm_amd import _lib
+    from flashgmm_amd import flash_gmm_native as C
+
+    cfg = CONFIGS[cid]
+    dev = torch.device("cuda:0")
+    X, mu0, var0, lp0 = make_problem(cid)
+    Xd = torch.from_numpy(X).to(dev)
+    mu = torch.from_numpy(mu0).to(dev)
+    var = torch.from_numpy(var0).to(dev)
+    lp = torch.from_numpy(lp0).to(dev)
+    lib = _lib.load()
+    vname = C.resolve_variant(cfg.N, cfg.K, cfg.d, variant)
+
+    # warmup (also builds the workspace)
+    if warmup > 0:
+        C.em_fit(Xd, mu, var, lp, warmup, variant=variant)
+    torch.cuda.synchronize()
+    _lib.check(lib.fgmm_profile_enable(1))
+    ms = (ctypes.c_double * 4)()
+    cnt = (ctypes.c_long * 4)()
+    _lib.check(lib.fgmm_profile_read(ms, cnt))  # reset
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    mu_o, var_o, lp_o, traj = C.em_fit(Xd, mu, var, lp, steps, variant=variant)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.check(lib.fgmm_profile_read(ms, cnt))
+    _lib.check(lib.fgmm_profile_enable(0))
+    # the same loop without events, for the headline number
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    C.em_fit(Xd, mu, var, lp, steps, variant=variant)
+    torch.cuda.synchronize()
+    elapsed_clean = time.perf_counter() - t0
+    ll = traj.cpu().numpy()
+    kern = {name: {"ms_avg": ms[i] / max(cnt[i], 1), "launches": int(cnt[i])}
+            for i, name in enumerate(["precompute", "pass1", "pass2", "reduce_mstep"])}
+    return {"elapsed": min(elapsed, elapsed_clean), "elapsed_profiled": elapsed,
+            "kernels": kern, "ll_first": float(ll[0]), "ll_last": float(ll[-1]),
+            "variant": vname}
+
+
+def cpu_baseline(cid, budget_s):
+    """Times the reference's standard E+M on the host (bounded sample)."""
+    import torch
+    from oracle import oracle as O
+
+    cfg = CONFIGS[cid]
+    cores = len(os.sched_getaffinity(0))
+    X, mu, var, lp = make_problem(cid)
+    ref = O.ref_module()
+    if ref is not None:
+        torch.set_num_threads(cores)
+        Xt, mut, vt, lpt = (torch.from_numpy(a) for a in (X, mu, var, lp))
+
+        def one():
+            g, _ = ref.standard_e_step(Xt, mut, vt, lpt)
+            ref.standard_m_step(Xt, g)
+        kind = "reference"
+    else:
+        def one():
+            O.c32_standard_em(X, mu, var, lp)
+        kind = "port"
+    one()  # warm-up iteration
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= cfg.iters:
+            break
+    per = float(np.mean(times))
+    return {"value": 1.0 / per, "unit": "EM iters/s", "cores": cores, "kind": kind,
+            "sample": f"{len(times)} standard E+M iteration(s) of C{cid} at full size "
+                      f"(N={cfg.N}, K={cfg.K}, d={cfg.d}) after 1 warm-up, "
+                      f"{per*1000:.1f} ms each"}
+
+
+def line_for(cid, args, with_cpu):
+    cfg = CONFIGS[cid]
+    r = run_gpu(cid, args.steps, args.warmup, args.variant)
+    sec = r["elapsed"]
+    its = args.steps / sec
+    p2 = r["kernels"]["pass2"]["ms_avg"] / 1e3
+    F_total = cfg.flops_per_iter()
+    roof_t = max(F_total / FP32_PEAK, cfg.bytes_per_iter() / HBM_PEAK)
+    achieved = pass2_flops(cfg) / p2 if p2 > 0 else 0.0
+    out = {
+        "metric": "EM iters/s (N=65536,K=256,d=128 fp32) + % of HBM / fp32-MFMA roofline",
+        "value": its,
+        "unit": "EM iters/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 (distance contraction in f64)",
+        "data": "synthetic (seeded mixture generator, flashgmm_amd/configs.py)",
+        "config": {"workload": f"C{cid}: diag-cov GMM EM N={cfg.N} K={cfg.K} d={cfg.d} fp32",
+                   "N": cfg.N, "K": cfg.K, "d": cfg.d, "kernel_variant": r["variant"]},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "pass2 (gamma recompute + sufficient statistics)",
+            "achieved": achieved / 1e12,
+            "peak": FP32_PEAK / 1e12,
+            "unit": "TFLOP/s",
+            "frac": achieved / FP32_PEAK,
+            "traffic": None,
+            "peak_at_kernel_precision": pass2_peak() / 1e12,
+            "frac_at_kernel_precision": achieved / pass2_peak(),
+        },
+        "iteration_roofline_frac": roof_t / (sec / args.steps),
+        "kernels_ms": {k: v["ms_avg"] for k, v in r["kernels"].items()},
+        "ll_first": r["ll_first"],
+        "ll_last": r["ll_last"],
+    }
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline(cid, args.cpu_seconds)
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the multi-GPU layout is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    rank = int(os.environ.get("RANK", "0"))
+    head = line_for(args.config, args, with_cpu=(rank == 0 and not args.no_cpu_baseline))
+    if rank == 0:
+        print(json.dumps(head), flush=True)
+    if args.all:
+        for cid in sorted(CONFIGS):
+            if cid == args.config:
+                continue
+            o = line_for(cid, args, with_cpu=False)
+            if rank == 0:
+                print(json.dumps(o), flush=True)
+
+
+if __name__ == "__main__":
+    main()

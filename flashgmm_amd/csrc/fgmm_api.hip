@@ -1,0 +1,366 @@
+// C ABI of libflashgmm: argument validation, problem geometry, workspace
+// layout, launch sequencing and optional per-kernel event timing.
+// Declarations and contracts: include/flashgmm.h.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/flashgmm.h"
+#include "fgmm_internal.h"
+
+namespace fgmm {
+
+hipError_t launch_pass1_mfma(const Geom&, const float*, const double*, const double*,
+                             double*, float*, double*, hipStream_t);
+hipError_t launch_pass2_mfma(const Geom&, const float*, const double*, const double*,
+                             const double*, float*, hipStream_t);
+hipError_t launch_pass1_valu(const Geom&, const float*, const double*, const double*,
+                             double*, float*, double*, hipStream_t);
+hipError_t launch_pass2_valu(const Geom&, const float*, const double*, const double*,
+                             const double*, float*, hipStream_t);
+
+static thread_local char g_err[512] = "";
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Variant table keyed by (K, d).  Matrix cores need >= 16 components to fill
+// a 16x16 tile (K is padded to 32) and hold the 16-component coefficient
+// fragment in registers up to d = 128; below or above that the vector-ALU
+// kernels run.
+static int resolve_variant(int K, int d, int variant) {
+  if (variant == kValu || variant == kMfma) return variant;
+  if (d <= 128 && K >= 16) return kMfma;
+  return kValu;
+}
+
+Geom make_geom(long N, int K, int d, int variant) {
+  Geom g;
+  g.N = N;
+  g.K = K;
+  g.d = d;
+  g.variant = resolve_variant(K, d, variant);
+  if (g.variant == kMfma) {
+    g.dp = round_up(d, 16);
+    g.Kp = round_up(K, 32);
+    g.p1_blocks = (int)((N + 127) / 128);
+    g.p2_kblocks = (g.Kp / 16 + 3) / 4;
+  } else {
+    int dp = 16;
+    while (dp < d) dp <<= 1;
+    g.dp = dp;
+    g.Kp = round_up(K, 16);
+    g.p1_blocks = (int)((N + 63) / 64);
+    g.p2_kblocks = (K + 7) / 8;
+  }
+  // Pass 2 splits the points into S chunks so that ~512 workgroups (two per
+  // CU) are in flight; each chunk leaves one fp32 partial row per component.
+  const long tile = 64;
+  long tiles = (N + tile - 1) / tile;
+  long S = (512 + g.p2_kblocks - 1) / g.p2_kblocks;
+  if (S > tiles) S = tiles;
+  if (S < 1) S = 1;
+  long chunk = round_up_l((N + S - 1) / S, tile);
+  g.p2_chunk = chunk;
+  g.p2_chunks = (int)((N + chunk - 1) / chunk);
+  g.stat_w = round_up(2 * g.dp + 1, 4);
+  return g;
+}
+
+WsLayout make_layout(const Geom& g) {
+  WsLayout L;
+  size_t off = 0;
+  L.params = off;
+  off = align256(off + sizeof(double) * 2 * (size_t)g.Kp * g.dp);
+  L.bias = off;
+  off = align256(off + sizeof(double) * (size_t)g.Kp);
+  L.ln2 = off;
+  off = align256(off + sizeof(double) * (size_t)g.N);
+  L.lnsum = off;
+  off = align256(off + sizeof(double) * (size_t)g.p1_blocks);
+  L.part = off;
+  off = align256(off + sizeof(float) * (size_t)g.p2_chunks * g.Kp * g.stat_w);
+  L.pbuf = off;
+  L.total = off;
+  return L;
+}
+
+// ---------------------------------------------------------------------------
+// event timing
+// ---------------------------------------------------------------------------
+namespace prof {
+constexpr int kKinds = 4;  // precompute, pass1, pass2, reduce/mstep
+constexpr int kCap = 16384;
+static bool enabled = false;
+static std::vector<hipEvent_t> ev;  // 2 per record
+static std::vector<int> kind;
+static int used = 0;
+static int ensure_pool() {
+  if (!ev.empty()) return 0;
+  ev.resize(2 * kCap);
+  kind.resize(kCap);
+  for (auto& e : ev)
+    if (hipEventCreate(&e) != hipSuccess) return -1;
+  return 0;
+}
+}  // namespace prof
+
+struct Timed {
+  int slot = -1;
+  hipStream_t s;
+  Timed(int k, hipStream_t st) : s(st) {
+    if (prof::enabled && prof::used < prof::kCap) {
+      slot = prof::used++;
+      prof::kind[slot] = k;
+      (void)hipEventRecord(prof::ev[2 * slot], s);
+    }
+  }
+  ~Timed() {
+    if (slot >= 0) (void)hipEventRecord(prof::ev[2 * slot + 1], s);
+  }
+};
+
+static int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FGMM_OK;
+  return fail(FGMM_EHIP, "HIP error in %s: %s", what, hipGetErrorString(e));
+}
+
+static int validate_shape(long N, int K, int d, int variant) {
+  if (N < 1) return fail(FGMM_EINVAL, "N must be >= 1 (got %ld)", N);
+  if (N > 2147483647L) return fail(FGMM_EINVAL, "N must be < 2^31 (got %ld)", N);
+  if (K < 1) return fail(FGMM_EINVAL, "K must be >= 1 (got %d)", K);
+  if (K > 65536) return fail(FGMM_EINVAL, "K must be <= 65536 (got %d)", K);
+  if (d < 1 || d > kMaxD)
+    return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
+  if (variant < 0 || variant > 2)
+    return fail(FGMM_EINVAL, "unknown variant %d", variant);
+  if (variant == kMfma && d > 128)
+    return fail(FGMM_EINVAL, "the MFMA variant supports d <= 128 (got %d)", d);
+  return FGMM_OK;
+}
+
+static int validate_ws(const Geom& g, const WsLayout& L, void* ws, size_t bytes) {
+  if (ws == nullptr) return fail(FGMM_EWORKSPACE, "workspace pointer is NULL");
+  if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0)
+    return fail(FGMM_EWORKSPACE, "workspace must be 256-byte aligned");
+  if (bytes < L.total)
+    return fail(FGMM_EWORKSPACE, "workspace too small: %zu bytes given, %zu needed", bytes,
+                L.total);
+  return FGMM_OK;
+}
+
+#define FGMM_REQUIRE(ptr) \
+  if ((ptr) == nullptr) return fail(FGMM_EINVAL, "%s must not be NULL", #ptr)
+
+struct Ws {
+  double* params;
+  double* bias;
+  double* ln2;
+  double* lnsum;
+  float* part;
+};
+
+static Ws carve(void* ws, const WsLayout& L) {
+  char* b = static_cast<char*>(ws);
+  return Ws{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
+            reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
+            reinterpret_cast<float*>(b + L.part)};
+}
+
+static int run_precompute(const Geom& g, const float* mu, const float* var,
+                          const float* lp, Ws& w, hipStream_t s) {
+  Timed t(0, s);
+  return check_hip(launch_precompute(g, mu, var, lp, w.params, w.bias, s), "precompute");
+}
+
+static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStream_t s) {
+  Timed t(1, s);
+  hipError_t e = g.variant == kMfma
+                     ? launch_pass1_mfma(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s)
+                     : launch_pass1_valu(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s);
+  return check_hip(e, "pass 1 (log-normalizer)");
+}
+
+static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
+  Timed t(2, s);
+  hipError_t e = g.variant == kMfma
+                     ? launch_pass2_mfma(g, X, w.params, w.bias, w.ln2, w.part, s)
+                     : launch_pass2_valu(g, X, w.params, w.bias, w.ln2, w.part, s);
+  return check_hip(e, "pass 2 (sufficient statistics)");
+}
+
+}  // namespace fgmm
+
+using namespace fgmm;
+
+extern "C" {
+
+int fgmm_version(void) { return 100; }
+
+const char* fgmm_last_error(void) { return g_err; }
+
+int fgmm_resolve_variant(long N, int K, int d, int variant) {
+  (void)N;
+  return resolve_variant(K, d, variant);
+}
+
+size_t fgmm_workspace_bytes(long N, int K, int d, int variant) {
+  if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
+  return make_layout(make_geom(N, K, d, variant)).total;
+}
+
+int fgmm_em_fused(const float* X, const float* mu, const float* var, const float* log_pi,
+                  long N, int K, int d, int variant, float* new_mu, float* new_var,
+                  float* new_log_pi, float* log_normalizer, void* ws, size_t ws_bytes,
+                  void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  FGMM_REQUIRE(new_mu); FGMM_REQUIRE(new_var); FGMM_REQUIRE(new_log_pi);
+  FGMM_REQUIRE(log_normalizer);
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(ws, L);
+  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
+  if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
+  if ((rc = run_pass2(g, X, w, s))) return rc;
+  Timed t(3, s);
+  return check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, new_mu,
+                                 new_var, new_log_pi, nullptr, nullptr, nullptr, s),
+                   "reduction / M-step");
+}
+
+int fgmm_log_normalizer(const float* X, const float* mu, const float* var,
+                        const float* log_pi, long N, int K, int d, int variant,
+                        float* log_normalizer, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  FGMM_REQUIRE(log_normalizer);
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(ws, L);
+  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
+  return run_pass1(g, X, w, log_normalizer, s);
+}
+
+int fgmm_accumulate_stats(const float* X, const float* mu, const float* var,
+                          const float* log_pi, const float* log_normalizer, long N, int K,
+                          int d, int variant, float* n_k, float* s_k, float* sq_k, void* ws,
+                          size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  FGMM_REQUIRE(log_normalizer); FGMM_REQUIRE(n_k); FGMM_REQUIRE(s_k); FGMM_REQUIRE(sq_k);
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(ws, L);
+  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
+  if ((rc = check_hip(launch_ln_to_ln2(N, log_normalizer, w.ln2, s), "ln conversion")))
+    return rc;
+  if ((rc = run_pass2(g, X, w, s))) return rc;
+  Timed t(3, s);
+  return check_hip(launch_reduce(g, w.part, w.lnsum, n_k, s_k, sq_k, nullptr, nullptr,
+                                 nullptr, nullptr, nullptr, nullptr, s),
+                   "statistics reduction");
+}
+
+int fgmm_m_step_update(const float* n_k, const float* s_k, const float* sq_k, long N, int K,
+                       int d, float* mu, float* var, float* log_pi, void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, kAuto);
+  if (rc) return rc;
+  FGMM_REQUIRE(n_k); FGMM_REQUIRE(s_k); FGMM_REQUIRE(sq_k);
+  FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  Geom g = make_geom(N, K, d, kAuto);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Timed t(3, s);
+  return check_hip(launch_mstep(g, n_k, s_k, sq_k, mu, var, log_pi, s), "M-step");
+}
+
+int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float* log_pi0,
+                long N, int K, int d, int iters, int variant, float* mu_out, float* var_out,
+                float* log_pi_out, double* ll_traj, void* ws, size_t ws_bytes,
+                void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  if (iters < 1) return fail(FGMM_EINVAL, "iters must be >= 1 (got %d)", iters);
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu0); FGMM_REQUIRE(var0); FGMM_REQUIRE(log_pi0);
+  FGMM_REQUIRE(mu_out); FGMM_REQUIRE(var_out); FGMM_REQUIRE(log_pi_out);
+  FGMM_REQUIRE(ll_traj);
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(ws, L);
+  if ((rc = run_precompute(g, mu0, var0, log_pi0, w, s))) return rc;
+  for (int it = 0; it < iters; it++) {
+    if ((rc = run_pass1(g, X, w, nullptr, s))) return rc;
+    if ((rc = run_pass2(g, X, w, s))) return rc;
+    Timed t(3, s);
+    // the M-step writes the fp32 parameters and, from their fp32 values, the
+    // coefficients the next iteration's passes read
+    rc = check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu_out,
+                                 var_out, log_pi_out, w.params, w.bias, ll_traj + it, s),
+                   "reduction / M-step");
+    if (rc) return rc;
+  }
+  return FGMM_OK;
+}
+
+int fgmm_profile_enable(int enable) {
+  g_err[0] = 0;
+  if (enable && prof::ensure_pool() != 0)
+    return fail(FGMM_EHIP, "hipEventCreate failed while enabling profiling");
+  prof::enabled = enable != 0;
+  return FGMM_OK;
+}
+
+int fgmm_profile_read(double* ms_total, long* launches) {
+  g_err[0] = 0;
+  FGMM_REQUIRE(ms_total);
+  FGMM_REQUIRE(launches);
+  for (int i = 0; i < prof::kKinds; i++) {
+    ms_total[i] = 0.0;
+    launches[i] = 0;
+  }
+  for (int i = 0; i < prof::used; i++) {
+    hipError_t e = hipEventSynchronize(prof::ev[2 * i + 1]);
+    if (e != hipSuccess) {
+      prof::used = 0;
+      return check_hip(e, "profile event wait");
+    }
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, prof::ev[2 * i], prof::ev[2 * i + 1]);
+    if (e != hipSuccess) {
+      prof::used = 0;
+      return check_hip(e, "profile event elapsed");
+    }
+    ms_total[prof::kind[i]] += ms;
+    launches[prof::kind[i]] += 1;
+  }
+  prof::used = 0;
+  return FGMM_OK;
+}
+
+}  // extern "C"

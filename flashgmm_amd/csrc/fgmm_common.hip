@@ -1,0 +1,251 @@
+// Coefficient precompute, fp64 reduction of the sufficient-statistic
+// partials fused with the M-step, and the standalone M-step.
+//
+// Reference formulas (file:line in the reference repository):
+//   inv_var / log_coeff   flash_gmm/csrc/flash_gmm_cuda.cu:40-57
+//   M-step + clamps       flash_gmm/csrc/flash_gmm_cuda.cu:298-322
+#include <float.h>
+#include <math.h>
+
+#include "fgmm_internal.h"
+
+namespace fgmm {
+
+// ---------------------------------------------------------------------------
+// Coefficients of one component.
+//
+// MFMA layout ("fragment order"): for 16-component subtile ks, MFMA step s
+// (0 <= s < dp/2) and lane l = 16*g + c of a 64-wide wavefront, element
+//     P[(ks*(dp/2) + s)*64 + l]
+// holds the coefficient of feature (s, g) for component 16*ks + c, where the
+// feature of step s < dp/4 is x_j^2 and of step s >= dp/4 is x_j, with
+// j = g*(dp/4) + (s mod dp/4).  Coefficients (base-2 log units):
+//     x_j^2 : -0.5*log2(e)/var_kj        x_j : log2(e)*mu_kj/var_kj
+//     bias_k = log2(e)*(log_coeff_k - 0.5*sum_j mu_kj^2/var_kj)
+// so that ll2_nk = bias_k + sum_f P[k][f] * feature_f(x_n).
+//
+// VALU layout: P[k*dp + j] = s_kj = sqrt(0.5*log2(e)/var_kj),
+//              P[Kp*dp + k*dp + j] = mu_kj*s_kj,  bias_k = log2(e)*log_coeff_k
+// so that ll2_nk = bias_k - sum_j (x_j*s_kj - mu_kj*s_kj)^2.
+// ---------------------------------------------------------------------------
+
+__device__ inline double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Block-wide fp64 sum for blockDim.x a multiple of 64 (<= 1024).
+__device__ inline double block_sum_f64(double v, double* red) {
+  v = wave_sum_f64(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < nw; i++) t += red[i];
+  return t;
+}
+
+// Writes the coefficients of component k (block-cooperative over j).
+// m / v are the fp32 parameter values of this component (nullptr for a
+// padding component, which gets zero coefficients and bias -inf).
+__device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
+                             const float* m, const float* v, float lp,
+                             double* P, double* bias, double* red) {
+  const bool real = (m != nullptr);
+  double lnv = 0.0, q = 0.0;
+  const int Q = dp / 4, S1 = dp / 2;
+  for (int j = threadIdx.x; j < dp; j += blockDim.x) {
+    double iv = 0.0, mu = 0.0;
+    if (real && j < d) {
+      double vv = (double)v[j];
+      iv = 1.0 / vv;
+      mu = (double)m[j];
+      lnv += log(vv);
+      q += mu * mu * iv;
+    }
+    if (variant == kMfma) {
+      const int ks = k >> 4, c = k & 15, g = j / Q, t = j - g * Q;
+      const int lane = 16 * g + c;
+      P[((size_t)ks * S1 + t) * 64 + lane] = -0.5 * kLog2e * iv;
+      P[((size_t)ks * S1 + Q + t) * 64 + lane] = kLog2e * mu * iv;
+    } else {
+      double sc = sqrt(0.5 * kLog2e * iv);
+      P[(size_t)k * dp + j] = sc;
+      P[(size_t)Kp * dp + (size_t)k * dp + j] = mu * sc;
+    }
+  }
+  lnv = block_sum_f64(lnv, red);
+  q = block_sum_f64(q, red);
+  if (threadIdx.x == 0) {
+    if (!real) {
+      bias[k] = -INFINITY;
+    } else {
+      double lc = (double)lp - 0.5 * ((double)d * kLog2Pi + lnv);
+      bias[k] = (variant == kMfma) ? kLog2e * (lc - 0.5 * q) : kLog2e * lc;
+    }
+  }
+}
+
+__global__ void precompute_kernel(int variant, int K, int Kp, int d, int dp,
+                                  const float* __restrict__ mu,
+                                  const float* __restrict__ var,
+                                  const float* __restrict__ log_pi,
+                                  double* __restrict__ P, double* __restrict__ bias) {
+  __shared__ double red[16];
+  const int k = blockIdx.x;
+  if (k < K)
+    write_coeffs(variant, k, Kp, d, dp, mu + (size_t)k * d, var + (size_t)k * d,
+                 log_pi[k], P, bias, red);
+  else
+    write_coeffs(variant, k, Kp, d, dp, nullptr, nullptr, 0.f, P, bias, red);
+}
+
+hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
+                             const float* log_pi, double* params, double* bias,
+                             hipStream_t s) {
+  hipLaunchKernelGGL(precompute_kernel, dim3(g.Kp), dim3(64), 0, s, g.variant, g.K,
+                     g.Kp, g.d, g.dp, mu, var, log_pi, params, bias);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Reduction of the Pass-2 partials + M-step.  One block per (padded)
+// component.  part[s][k][f]: f < dp -> sum gamma*x_j, dp <= f < 2dp ->
+// sum gamma*x_j^2, f = 2dp -> sum gamma.  Sums over s run in fp64 in a fixed
+// order, so results are bitwise reproducible.
+// ---------------------------------------------------------------------------
+__global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
+                              int S, int stat_w, const float* __restrict__ part,
+                              const double* __restrict__ lnsum, int n_lnsum,
+                              float* __restrict__ n_k, float* __restrict__ s_k,
+                              float* __restrict__ sq_k, float* __restrict__ new_mu,
+                              float* __restrict__ new_var,
+                              float* __restrict__ new_log_pi,
+                              double* __restrict__ P_next, double* __restrict__ bias_next,
+                              double* __restrict__ ll_out) {
+  __shared__ double red[16];
+  __shared__ double nk_sh;
+  __shared__ float mu_sh[kMaxD], var_sh[kMaxD];
+  const int k = blockIdx.x;
+
+  if (k == 0 && ll_out != nullptr) {
+    double t = 0.0;
+    for (int i = threadIdx.x; i < n_lnsum; i += blockDim.x) t += lnsum[i];
+    t = block_sum_f64(t, red);
+    if (threadIdx.x == 0) ll_out[0] = t / (double)N;
+  }
+
+  if (k >= K) {  // padding components only need coefficients for the next pass
+    if (P_next != nullptr)
+      write_coeffs(variant, k, Kp, d, dp, nullptr, nullptr, 0.f, P_next, bias_next, red);
+    return;
+  }
+
+  const size_t row = (size_t)stat_w;
+  const size_t kstride = (size_t)Kp * row;
+  {
+    // n_k: chunk partials split across the block, merged in a fixed order
+    double t = 0.0;
+    const float* p = part + (size_t)k * row + 2 * dp;
+    for (int s = threadIdx.x; s < S; s += blockDim.x) t += (double)p[(size_t)s * kstride];
+    t = block_sum_f64(t, red);
+    if (threadIdx.x == 0) nk_sh = t;
+  }
+  __syncthreads();
+  const double nk = nk_sh;
+  const double inv = 1.0 / (nk > 1e-8 ? nk : 1e-8);
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    double a = 0.0, b = 0.0;
+    const float* p = part + (size_t)k * row;
+#pragma unroll 8
+    for (int s = 0; s < S; s++) {
+      a += (double)p[(size_t)s * kstride + j];
+      b += (double)p[(size_t)s * kstride + dp + j];
+    }
+    if (s_k != nullptr) {
+      s_k[(size_t)k * d + j] = (float)a;
+      sq_k[(size_t)k * d + j] = (float)b;
+    }
+    if (new_mu != nullptr) {
+      double m = a * inv;
+      double v = b * inv - m * m;
+      v = v > 1e-6 ? v : 1e-6;
+      float mf = (float)m, vf = (float)v;
+      new_mu[(size_t)k * d + j] = mf;
+      new_var[(size_t)k * d + j] = vf;
+      mu_sh[j] = mf;
+      var_sh[j] = vf;
+    }
+  }
+  float lpf = 0.f;
+  if (new_log_pi != nullptr) {
+    double p = nk / (double)N;
+    lpf = (float)log(p > 1e-8 ? p : 1e-8);
+    if (threadIdx.x == 0) new_log_pi[k] = lpf;
+  }
+  if (n_k != nullptr && threadIdx.x == 0) n_k[k] = (float)nk;
+  if (P_next != nullptr) {
+    __syncthreads();
+    write_coeffs(variant, k, Kp, d, dp, mu_sh, var_sh, lpf, P_next, bias_next, red);
+  }
+}
+
+hipError_t launch_reduce(const Geom& g, const float* part, const double* lnsum,
+                         float* n_k, float* s_k, float* sq_k, float* new_mu,
+                         float* new_var, float* new_log_pi, double* params_next,
+                         double* bias_next, double* ll_out, hipStream_t s) {
+  const int blocks = params_next != nullptr ? g.Kp : g.K;
+  hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
+                     g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
+                     n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
+                     bias_next, ll_out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Standalone M-step on fp32 statistics (flash_gmm_cuda.cu:298-322 semantics,
+// evaluated in fp64 and rounded once).
+// ---------------------------------------------------------------------------
+__global__ void mstep_kernel(long N, int K, int d, const float* __restrict__ n_k,
+                             const float* __restrict__ s_k,
+                             const float* __restrict__ sq_k, float* __restrict__ mu,
+                             float* __restrict__ var, float* __restrict__ log_pi) {
+  const int k = blockIdx.x;
+  const double nk = (double)n_k[k];
+  const double inv = 1.0 / (nk > 1e-8 ? nk : 1e-8);
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    double m = (double)s_k[(size_t)k * d + j] * inv;
+    double v = (double)sq_k[(size_t)k * d + j] * inv - m * m;
+    mu[(size_t)k * d + j] = (float)m;
+    var[(size_t)k * d + j] = (float)(v > 1e-6 ? v : 1e-6);
+  }
+  if (threadIdx.x == 0) {
+    double p = nk / (double)N;
+    log_pi[k] = (float)log(p > 1e-8 ? p : 1e-8);
+  }
+}
+
+hipError_t launch_mstep(const Geom& g, const float* n_k, const float* s_k,
+                        const float* sq_k, float* mu, float* var, float* log_pi,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(mstep_kernel, dim3(g.K), dim3(128), 0, s, g.N, g.K, g.d, n_k, s_k,
+                     sq_k, mu, var, log_pi);
+  return hipGetLastError();
+}
+
+// fp32 natural-log normalizer supplied by a caller -> internal fp64 base-2.
+__global__ void ln_to_ln2_kernel(long N, const float* __restrict__ ln,
+                                 double* __restrict__ ln2) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < N) ln2[i] = (double)ln[i] * kLog2e;
+}
+
+hipError_t launch_ln_to_ln2(long N, const float* ln, double* ln2, hipStream_t s) {
+  const int blocks = (int)((N + 255) / 256);
+  hipLaunchKernelGGL(ln_to_ln2_kernel, dim3(blocks), dim3(256), 0, s, N, ln, ln2);
+  return hipGetLastError();
+}
+
+}  // namespace fgmm

@@ -1,0 +1,87 @@
+// Internal declarations shared by the HIP translation units of libflashgmm.
+//
+// Conventions used by every kernel in this library
+// ------------------------------------------------
+// * All log-likelihood arithmetic runs in base 2: ll2 = log2(e) * ll.  The
+//   precomputed parameters carry the log2(e) factor, so exp2 / log2 map to
+//   the hardware's v_exp_f32 / v_log_f32 without an extra multiply.
+// * The distance contraction is evaluated in fp64 (the benchmark's parity
+//   bar on mu/var is 1e-5 absolute, which fp32 distance arithmetic cannot
+//   reach at the headline shape); responsibilities and the sufficient
+//   statistics GEMM run in fp32; cross-workgroup sums and the M-step in fp64.
+// * Padded dimensions: d is padded to dp (multiple of 16) with zero
+//   features; K is padded to Kp (multiple of 16) with components whose bias
+//   is -inf, so they receive exactly zero responsibility.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fgmm {
+
+constexpr int kMaxD = 256;          // same dimension limit as the reference kernels
+constexpr double kLog2e = 1.4426950408889634073599246810019;
+constexpr double kLn2 = 0.69314718055994530941723212145818;
+constexpr double kLog2Pi = 1.8378770664093454835606594728112;  // ln(2*pi)
+
+inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+inline long round_up_l(long x, long m) { return (x + m - 1) / m * m; }
+
+enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2 };
+
+// Geometry of one problem, derived once per call on the host.
+struct Geom {
+  long N;
+  int K, d;
+  int dp;       // d padded to a multiple of 16
+  int Kp;       // K padded to a multiple of 16
+  int variant;  // resolved (kValu or kMfma)
+  // pass 1
+  int p1_blocks;
+  // pass 2
+  int p2_kblocks;   // grid.x
+  int p2_chunks;    // grid.y (S): point chunks, one stats partial each
+  long p2_chunk;    // points per chunk (multiple of the point tile)
+  int stat_w;       // row width of a stats partial (2*dp + 1 padded to 4)
+};
+
+// Byte offsets of the workspace regions (all 256-byte aligned).
+struct WsLayout {
+  size_t params;    // fp64 fragment-ordered coefficients (MFMA) or s/mu*s (VALU)
+  size_t bias;      // fp64 [Kp]
+  size_t ln2;       // fp64 [N]   base-2 log-normalizer
+  size_t lnsum;     // fp64 [p1_blocks] per-workgroup sums of ln (natural)
+  size_t part;      // fp32 [S][Kp][stat_w] sufficient-statistic partials
+  size_t pbuf;      // fp32 ping-pong parameter buffers for the device EM loop
+  size_t total;
+};
+
+Geom make_geom(long N, int K, int d, int variant);
+WsLayout make_layout(const Geom& g);
+
+// ---- kernel launchers (defined in the .hip files) ----
+hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
+                             const float* log_pi, double* params, double* bias,
+                             hipStream_t s);
+hipError_t launch_pass1(const Geom& g, const float* X, const double* params,
+                        const double* bias, double* ln2, float* ln_out,
+                        double* lnsum, hipStream_t s);
+hipError_t launch_pass2(const Geom& g, const float* X, const double* params,
+                        const double* bias, const double* ln2, float* part,
+                        hipStream_t s);
+// Reduces the stats partials in fp64.  Writes any of: fp32 stats
+// (n_k, s_k, sq_k), fp32 new parameters (M-step with the native clamps),
+// the precomputed coefficients for the next iteration (params_next/bias_next),
+// and ll_out = sum(lnsum)/N.
+hipError_t launch_reduce(const Geom& g, const float* part, const double* lnsum,
+                         float* n_k, float* s_k, float* sq_k, float* new_mu,
+                         float* new_var, float* new_log_pi, double* params_next,
+                         double* bias_next, double* ll_out, hipStream_t s);
+// Caller-supplied fp32 natural-log normalizer -> internal fp64 base-2 copy.
+hipError_t launch_ln_to_ln2(long N, const float* ln, double* ln2, hipStream_t s);
+// Standalone M-step on caller-provided fp32 statistics.
+hipError_t launch_mstep(const Geom& g, const float* n_k, const float* s_k,
+                        const float* sq_k, float* mu, float* var, float* log_pi,
+                        hipStream_t s);
+
+}  // namespace fgmm

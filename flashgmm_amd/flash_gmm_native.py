@@ -1,0 +1,190 @@
+"""Drop-in for the reference's ``flash_gmm_native`` extension module on ROCm.
+
+Same function names, argument order, defaults and return order as the
+reference's pybind11 module (``flash_gmm/csrc/binding.cpp:94-109``), plus the
+three stage entry points (``flash_log_normalizer``, ``flash_accumulate_stats``,
+``m_step_update``).  Every call goes to ``libflashgmm.so`` (hand-written HIP
+kernels for gfx950) on torch's current stream; tensors must live on a ROCm
+device.  Outputs are fresh tensors; inputs are never modified.
+
+Errors are ``RuntimeError`` like the reference's ``TORCH_CHECK``; the dtype
+check keeps the reference's message ("X must be float32",
+``binding.cpp:38,54,65,80``).  Unlike the reference, shapes, devices,
+``d <= 256`` and launch failures are checked too, before any device work.
+
+The reference dispatches CPU tensors to its OpenMP path
+(``binding.cpp:48,59,75,91``).  This module accelerates the ROCm path only and
+raises on CPU tensors instead of computing elsewhere.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _check_device(X: torch.Tensor, fn: str) -> None:
+    if not X.is_cuda:
+        raise RuntimeError(
+            f"flashgmm_amd.{fn}: tensors must be on a ROCm device (got {X.device}); "
+            "this module has no CPU implementation")
+
+
+def _params(X, mu, var, log_pi, fn):
+    """Validates (X, mu, var, log_pi); returns contiguous fp32 views and (N, K, d)."""
+    if X.dtype != torch.float32:
+        raise RuntimeError("X must be float32")
+    if X.dim() != 2:
+        raise RuntimeError("X must be 2D")
+    _check_device(X, fn)
+    N, d = X.shape
+    if N < 1 or d < 1:
+        raise RuntimeError(f"flashgmm_amd.{fn}: X must be non-empty (got {tuple(X.shape)})")
+    if d > 256:
+        raise RuntimeError(f"flashgmm_amd.{fn}: d must be <= 256 (got {d})")
+    if mu.dim() != 2 or mu.shape[1] != d:
+        raise RuntimeError(f"flashgmm_amd.{fn}: mu must be [K, {d}] (got {tuple(mu.shape)})")
+    K = mu.shape[0]
+    if K < 1:
+        raise RuntimeError(f"flashgmm_amd.{fn}: K must be >= 1")
+    if tuple(var.shape) != (K, d):
+        raise RuntimeError(f"flashgmm_amd.{fn}: var must be [{K}, {d}] (got {tuple(var.shape)})")
+    if tuple(log_pi.shape) != (K,):
+        raise RuntimeError(f"flashgmm_amd.{fn}: log_pi must be [{K}] (got {tuple(log_pi.shape)})")
+    out = []
+    for name, t in (("mu", mu), ("var", var), ("log_pi", log_pi)):
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"flashgmm_amd.{fn}: {name} must be float32 (got {t.dtype})")
+        if t.device != X.device:
+            raise RuntimeError(f"flashgmm_amd.{fn}: {name} is on {t.device}, X on {X.device}")
+        out.append(t.contiguous())
+    return (X.contiguous(), *out, N, K, d)
+
+
+def _ws(X, N, K, d, variant):
+    lib = _lib.load()
+    nbytes = lib.fgmm_workspace_bytes(N, K, d, variant)
+    if nbytes == 0:
+        raise RuntimeError(f"flashgmm_amd: unsupported problem N={N} K={K} d={d} "
+                           f"variant={variant}")
+    return _lib.workspace(X.device, nbytes), nbytes
+
+
+def flash_em_fused(X, mu, var, log_pi, BN: int = 64, BK: int = 8, *, variant=None):
+    """One fused EM iteration; returns ``[new_mu, new_var, new_log_pi,
+    log_normalizer]`` (``binding.cpp:62-76,102-105``,
+    ``flash_gmm_cuda.cu:402-504``).  ``BN``/``BK`` are accepted for signature
+    compatibility; the gfx950 kernels pick their own tiles per (K, d)."""
+    if int(BN) < 1 or int(BK) < 1:
+        raise RuntimeError(f"flashgmm_amd.flash_em_fused: BN and BK must be >= 1 (got {BN}, {BK})")
+    X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, "flash_em_fused")
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
+    new_mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    new_var = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    new_log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
+    ln = torch.empty((N,), dtype=torch.float32, device=X.device)
+    _lib.check(lib.fgmm_em_fused(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, v,
+                                 _ptr(new_mu), _ptr(new_var), _ptr(new_log_pi), _ptr(ln),
+                                 _ptr(ws), nbytes, _lib.stream_handle(X.device)))
+    return [new_mu, new_var, new_log_pi, ln]
+
+
+def flash_log_normalizer(X, mu, var, log_pi, *, variant=None):
+    """Pass 1: ``log_normalizer[n] = logsumexp_k(log pi_k + log N(x_n | mu_k, var_k))``
+    (``flash_gmm_cuda.cu:72-170``; ``flash_e_step.py:144-177``)."""
+    X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, "flash_log_normalizer")
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
+    ln = torch.empty((N,), dtype=torch.float32, device=X.device)
+    _lib.check(lib.fgmm_log_normalizer(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, v,
+                                       _ptr(ln), _ptr(ws), nbytes,
+                                       _lib.stream_handle(X.device)))
+    return ln
+
+
+def flash_accumulate_stats(X, mu, var, log_pi, log_normalizer, *, variant=None):
+    """Pass 2: returns ``[n_k, s_k, sq_k]`` with gamma recomputed on chip
+    (``flash_gmm_cuda.cu:179-292``; ``flash_e_step.py:179-219``)."""
+    X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, "flash_accumulate_stats")
+    if tuple(log_normalizer.shape) != (N,) or log_normalizer.dtype != torch.float32:
+        raise RuntimeError(f"flashgmm_amd.flash_accumulate_stats: log_normalizer must be "
+                           f"float32 [{N}] (got {log_normalizer.dtype} "
+                           f"{tuple(log_normalizer.shape)})")
+    if log_normalizer.device != X.device:
+        raise RuntimeError("flashgmm_amd.flash_accumulate_stats: log_normalizer is on "
+                           f"{log_normalizer.device}, X on {X.device}")
+    ln = log_normalizer.contiguous()
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
+    n_k = torch.empty((K,), dtype=torch.float32, device=X.device)
+    s_k = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    sq_k = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    _lib.check(lib.fgmm_accumulate_stats(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(ln),
+                                         N, K, d, v, _ptr(n_k), _ptr(s_k), _ptr(sq_k),
+                                         _ptr(ws), nbytes, _lib.stream_handle(X.device)))
+    return [n_k, s_k, sq_k]
+
+
+def m_step_update(n_k, s_k, sq_k, N: int):
+    """M-step from sufficient statistics with the native clamps; returns
+    ``[mu, var, log_pi]`` (``flash_gmm_cuda.cu:298-322``)."""
+    for name, t in (("n_k", n_k), ("s_k", s_k), ("sq_k", sq_k)):
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"flashgmm_amd.m_step_update: {name} must be float32")
+    _check_device(s_k, "m_step_update")
+    if s_k.dim() != 2:
+        raise RuntimeError("flashgmm_amd.m_step_update: s_k must be [K, d]")
+    K, d = s_k.shape
+    if tuple(n_k.shape) != (K,) or tuple(sq_k.shape) != (K, d):
+        raise RuntimeError("flashgmm_amd.m_step_update: expected n_k [K], s_k/sq_k [K, d]")
+    if n_k.device != s_k.device or sq_k.device != s_k.device:
+        raise RuntimeError("flashgmm_amd.m_step_update: statistics on different devices")
+    N = int(N)
+    if N < 1:
+        raise RuntimeError("flashgmm_amd.m_step_update: N must be >= 1")
+    lib = _lib.load()
+    mu = torch.empty((K, d), dtype=torch.float32, device=s_k.device)
+    var = torch.empty((K, d), dtype=torch.float32, device=s_k.device)
+    log_pi = torch.empty((K,), dtype=torch.float32, device=s_k.device)
+    _lib.check(lib.fgmm_m_step_update(_ptr(n_k.contiguous()), _ptr(s_k.contiguous()),
+                                      _ptr(sq_k.contiguous()), N, K, d, _ptr(mu), _ptr(var),
+                                      _ptr(log_pi), _lib.stream_handle(s_k.device)))
+    return [mu, var, log_pi]
+
+
+def em_fit(X, mu0, var0, log_pi0, iters: int, *, variant=None):
+    """``iters`` fused EM iterations on the device with no host round trip.
+
+    Returns ``(mu, var, log_pi, ll_traj)``; ``ll_traj[it]`` (float64, on the
+    device) is the mean log-normalizer under the parameters entering
+    iteration ``it`` -- ``NativeFlashGMM.fit``'s per-iteration
+    ``log_likelihood`` (``native_wrapper.py:128-137``)."""
+    X, mu0, var0, log_pi0, N, K, d = _params(X, mu0, var0, log_pi0, "em_fit")
+    iters = int(iters)
+    if iters < 1:
+        raise RuntimeError("flashgmm_amd.em_fit: iters must be >= 1")
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
+    mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    var = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
+    traj = torch.empty((iters,), dtype=torch.float64, device=X.device)
+    _lib.check(lib.fgmm_em_fit(_ptr(X), _ptr(mu0), _ptr(var0), _ptr(log_pi0), N, K, d, iters, v,
+                               _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(traj), _ptr(ws), nbytes,
+                               _lib.stream_handle(X.device)))
+    return mu, var, log_pi, traj
+
+
+def resolve_variant(N: int, K: int, d: int, variant=None) -> str:
+    """Name of the kernel family the library runs for this shape."""
+    code = _lib.load().fgmm_resolve_variant(int(N), int(K), int(d), _lib.variant_code(variant))
+    return {1: "valu", 2: "mfma"}[code]

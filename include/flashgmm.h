@@ -1,0 +1,135 @@
+/*
+ * flashgmm.h -- C ABI of libflashgmm.so, the MI355X (gfx950) implementation of
+ * Flash-GMM's fused diagonal-covariance EM iteration.
+ *
+ * Plain pointers and sizes only.  Every tensor argument is a DEVICE pointer
+ * to a C-contiguous fp32 array (row-major), except where noted.  `stream` is
+ * a hipStream_t passed as void* (NULL = the null stream).  Calls are
+ * asynchronous on `stream`; output buffers are valid once the stream has
+ * reached the call.  Inputs are never written.
+ *
+ * Shapes: X[N][d], mu[K][d], var[K][d], log_pi[K] (natural log of the
+ * mixture weights), log_normalizer[N], n_k[K], s_k[K][d], sq_k[K][d].
+ * Limits: N >= 1, K >= 1, 1 <= d <= 256 (the reference kernels' own limit,
+ * flash_gmm/csrc/flash_gmm_cuda.cu:22, enforced here instead of silently
+ * dropping dimensions).
+ *
+ * Return value: FGMM_OK (0) or one of the FGMM_E* codes below;
+ * fgmm_last_error() returns a message for the calling thread's last failure.
+ * Argument errors are detected before any device work is queued.
+ *
+ * Workspace: entry points that take (ws, ws_bytes) need a device buffer of at
+ * least fgmm_workspace_bytes(N, K, d, variant) bytes, 256-byte aligned.  The
+ * library allocates no device memory of its own on these paths.
+ *
+ * variant: FGMM_VARIANT_AUTO picks matrix-core or vector-ALU kernels from a
+ * table keyed by (K, d); FGMM_VARIANT_VALU / FGMM_VARIANT_MFMA force one.
+ */
+#ifndef FLASHGMM_H
+#define FLASHGMM_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FGMM_OK 0
+#define FGMM_EINVAL 1      /* bad argument (shape, null pointer, limit)   */
+#define FGMM_EWORKSPACE 2  /* workspace too small or misaligned           */
+#define FGMM_EHIP 3        /* HIP runtime / launch error                  */
+
+#define FGMM_VARIANT_AUTO 0
+#define FGMM_VARIANT_VALU 1
+#define FGMM_VARIANT_MFMA 2
+
+/* Library ABI version (major*100 + minor). */
+int fgmm_version(void);
+
+/* Message describing the calling thread's last error ("" if none). */
+const char* fgmm_last_error(void);
+
+/* Variant the library will run for (K, d) when asked for `variant`. */
+int fgmm_resolve_variant(long N, int K, int d, int variant);
+
+/* Workspace bytes needed by every entry point below for this problem. */
+size_t fgmm_workspace_bytes(long N, int K, int d, int variant);
+
+/*
+ * One fused EM iteration: precompute -> Pass 1 (log-normalizer) -> Pass 2
+ * (sufficient statistics) -> M-step.  Outputs new_mu[K][d], new_var[K][d],
+ * new_log_pi[K] and log_normalizer[N] (= log p(x_n) under the INPUT
+ * parameters).  M-step clamps: 1/max(n_k,1e-8), var >= 1e-6,
+ * log(max(n_k/N,1e-8)).
+ * Replaces flash_em_fused_cuda (flash_gmm/csrc/flash_gmm_cuda.cu:402-504),
+ * bound as flash_em_fused in flash_gmm/csrc/binding.cpp:62-76,102-105.
+ * The reference's BN/BK launch hints have no counterpart here: tile shapes
+ * are fixed per (K, d) for gfx950.
+ */
+int fgmm_em_fused(const float* X, const float* mu, const float* var,
+                  const float* log_pi, long N, int K, int d, int variant,
+                  float* new_mu, float* new_var, float* new_log_pi,
+                  float* log_normalizer, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Pass 1 alone: log_normalizer[n] = logsumexp_k(log pi_k + log N(x_n|mu_k,var_k)).
+ * Replaces flash_log_normalizer_v2_kernel (flash_gmm/csrc/flash_gmm_cuda.cu:72-170);
+ * the Python reference splits the same stage out as the first half of
+ * flash_e_step_no_gamma (flash_gmm/flash_e_step.py:144-177).
+ */
+int fgmm_log_normalizer(const float* X, const float* mu, const float* var,
+                        const float* log_pi, long N, int K, int d, int variant,
+                        float* log_normalizer, void* ws, size_t ws_bytes,
+                        void* stream);
+
+/*
+ * Pass 2 alone: gamma_nk = exp(ll_nk - log_normalizer_n) recomputed on chip;
+ * n_k = sum_n gamma, s_k = sum_n gamma x, sq_k = sum_n gamma x^2.
+ * `log_normalizer` is the caller's fp32 Pass-1 output.
+ * Replaces flash_accumulate_stats_v2_kernel (flash_gmm/csrc/flash_gmm_cuda.cu:179-292),
+ * the second half of flash_e_step_no_gamma (flash_gmm/flash_e_step.py:179-219).
+ */
+int fgmm_accumulate_stats(const float* X, const float* mu, const float* var,
+                          const float* log_pi, const float* log_normalizer, long N,
+                          int K, int d, int variant, float* n_k, float* s_k,
+                          float* sq_k, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * M-step from sufficient statistics, native clamps as above.
+ * Replaces update_params_kernel (flash_gmm/csrc/flash_gmm_cuda.cu:298-322).
+ */
+int fgmm_m_step_update(const float* n_k, const float* s_k, const float* sq_k,
+                       long N, int K, int d, float* mu, float* var, float* log_pi,
+                       void* stream);
+
+/*
+ * `iters` fused EM iterations back to back on the device, parameters fed
+ * forward on the device (fp32 between iterations, as the per-call API keeps
+ * them).  ll_traj[it] (HOST-readable only after the stream completes; a
+ * DEVICE pointer to `iters` doubles) = mean_n log_normalizer under the
+ * parameters entering iteration it -- the quantity NativeFlashGMM.fit
+ * records per iteration (flash_gmm/native_wrapper.py:128-137) without its
+ * per-iteration host synchronisation.  No early stop (tol = 0).
+ * mu0/var0/log_pi0 may alias mu_out/var_out/log_pi_out.
+ */
+int fgmm_em_fit(const float* X, const float* mu0, const float* var0,
+                const float* log_pi0, long N, int K, int d, int iters, int variant,
+                float* mu_out, float* var_out, float* log_pi_out, double* ll_traj,
+                void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Kernel timing with HIP events recorded on the launch stream around every
+ * kernel this library queues, while enabled.  fgmm_profile_read waits for
+ * the recorded events, then fills ms_total[i] and launches[i] for
+ * i = 0 precompute, 1 Pass 1, 2 Pass 2, 3 reduction/M-step, and resets.
+ * No counterpart in the reference (its benchmark brackets whole calls with
+ * CUDA events, flash_gmm/benchmark_gpu.py:25-44).
+ */
+int fgmm_profile_enable(int enable);
+int fgmm_profile_read(double* ms_total, long* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHGMM_H */
