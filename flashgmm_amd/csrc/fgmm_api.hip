@@ -16,11 +16,11 @@ namespace fgmm {
 hipError_t launch_pass1_mfma(const Geom&, const float*, const double*, const double*,
                              double*, float*, double*, hipStream_t);
 hipError_t launch_pass2_mfma(const Geom&, const float*, const double*, const double*,
-                             const double*, float*, hipStream_t);
+                             const double*, double*, hipStream_t);
 hipError_t launch_pass1_valu(const Geom&, const float*, const double*, const double*,
                              double*, float*, double*, hipStream_t);
 hipError_t launch_pass2_valu(const Geom&, const float*, const double*, const double*,
-                             const double*, float*, hipStream_t);
+                             const double*, double*, hipStream_t);
 
 static thread_local char g_err[512] = "";
 
@@ -64,10 +64,12 @@ Geom make_geom(long N, int K, int d, int variant) {
     g.p2_kblocks = (K + 7) / 8;
   }
   // Pass 2 splits the points into S chunks so that ~512 workgroups (two per
-  // CU) are in flight; each chunk leaves one fp32 partial row per component.
+  // CU) are in flight; each chunk leaves one fp64 partial row per component.
+  // Chunks stay <= 4096 points so the fp32 sum of gamma*x stays short.
   const long tile = 64;
   long tiles = (N + tile - 1) / tile;
   long S = (512 + g.p2_kblocks - 1) / g.p2_kblocks;
+  if (S < (N + 4095) / 4096) S = (N + 4095) / 4096;
   if (S > tiles) S = tiles;
   if (S < 1) S = 1;
   long chunk = round_up_l((N + S - 1) / S, tile);
@@ -89,7 +91,7 @@ WsLayout make_layout(const Geom& g) {
   L.lnsum = off;
   off = align256(off + sizeof(double) * (size_t)g.p1_blocks);
   L.part = off;
-  off = align256(off + sizeof(float) * (size_t)g.p2_chunks * g.Kp * g.stat_w);
+  off = align256(off + sizeof(double) * (size_t)g.p2_chunks * g.Kp * g.stat_w);
   L.pbuf = off;
   L.total = off;
   return L;
@@ -167,14 +169,14 @@ struct Ws {
   double* bias;
   double* ln2;
   double* lnsum;
-  float* part;
+  double* part;
 };
 
 static Ws carve(void* ws, const WsLayout& L) {
   char* b = static_cast<char*>(ws);
   return Ws{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
             reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
-            reinterpret_cast<float*>(b + L.part)};
+            reinterpret_cast<double*>(b + L.part)};
 }
 
 static int run_precompute(const Geom& g, const float* mu, const float* var,

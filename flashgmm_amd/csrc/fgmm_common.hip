@@ -112,12 +112,12 @@ hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
 
 // ---------------------------------------------------------------------------
 // Reduction of the Pass-2 partials + M-step.  One block per (padded)
-// component.  part[s][k][f]: f < dp -> sum gamma*x_j, dp <= f < 2dp ->
-// sum gamma*x_j^2, f = 2dp -> sum gamma.  Sums over s run in fp64 in a fixed
+// component.  part[s][k][f] (fp64): f < dp -> sum gamma*x_j,
+// dp <= f < 2dp -> sum gamma*x_j^2, f = 2dp -> sum gamma.  Sums over s run in fp64 in a fixed
 // order, so results are bitwise reproducible.
 // ---------------------------------------------------------------------------
 __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
-                              int S, int stat_w, const float* __restrict__ part,
+                              int S, int stat_w, const double* __restrict__ part,
                               const double* __restrict__ lnsum, int n_lnsum,
                               float* __restrict__ n_k, float* __restrict__ s_k,
                               float* __restrict__ sq_k, float* __restrict__ new_mu,
@@ -148,8 +148,8 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   {
     // n_k: chunk partials split across the block, merged in a fixed order
     double t = 0.0;
-    const float* p = part + (size_t)k * row + 2 * dp;
-    for (int s = threadIdx.x; s < S; s += blockDim.x) t += (double)p[(size_t)s * kstride];
+    const double* p = part + (size_t)k * row + 2 * dp;
+    for (int s = threadIdx.x; s < S; s += blockDim.x) t += p[(size_t)s * kstride];
     t = block_sum_f64(t, red);
     if (threadIdx.x == 0) nk_sh = t;
   }
@@ -158,11 +158,11 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   const double inv = 1.0 / (nk > 1e-8 ? nk : 1e-8);
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
     double a = 0.0, b = 0.0;
-    const float* p = part + (size_t)k * row;
+    const double* p = part + (size_t)k * row;
 #pragma unroll 8
     for (int s = 0; s < S; s++) {
-      a += (double)p[(size_t)s * kstride + j];
-      b += (double)p[(size_t)s * kstride + dp + j];
+      a += p[(size_t)s * kstride + j];
+      b += p[(size_t)s * kstride + dp + j];
     }
     if (s_k != nullptr) {
       s_k[(size_t)k * d + j] = (float)a;
@@ -192,7 +192,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   }
 }
 
-hipError_t launch_reduce(const Geom& g, const float* part, const double* lnsum,
+hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s) {

@@ -7,8 +7,9 @@
 //   the hardware's v_exp_f32 / v_log_f32 without an extra multiply.
 // * The distance contraction is evaluated in fp64 (the benchmark's parity
 //   bar on mu/var is 1e-5 absolute, which fp32 distance arithmetic cannot
-//   reach at the headline shape); responsibilities and the sufficient
-//   statistics GEMM run in fp32; cross-workgroup sums and the M-step in fp64.
+//   reach at the headline shape); responsibilities are fp32; sum gamma*x is
+//   accumulated in fp32, sum gamma*x^2 and sum gamma in fp64 (x^2 is exact
+//   in fp64); cross-workgroup sums and the M-step run in fp64.
 // * Padded dimensions: d is padded to dp (multiple of 16) with zero
 //   features; K is padded to Kp (multiple of 16) with components whose bias
 //   is -inf, so they receive exactly zero responsibility.
@@ -51,7 +52,7 @@ struct WsLayout {
   size_t bias;      // fp64 [Kp]
   size_t ln2;       // fp64 [N]   base-2 log-normalizer
   size_t lnsum;     // fp64 [p1_blocks] per-workgroup sums of ln (natural)
-  size_t part;      // fp32 [S][Kp][stat_w] sufficient-statistic partials
+  size_t part;      // fp64 [S][Kp][stat_w] sufficient-statistic partials
   size_t pbuf;      // fp32 ping-pong parameter buffers for the device EM loop
   size_t total;
 };
@@ -67,13 +68,13 @@ hipError_t launch_pass1(const Geom& g, const float* X, const double* params,
                         const double* bias, double* ln2, float* ln_out,
                         double* lnsum, hipStream_t s);
 hipError_t launch_pass2(const Geom& g, const float* X, const double* params,
-                        const double* bias, const double* ln2, float* part,
+                        const double* bias, const double* ln2, double* part,
                         hipStream_t s);
 // Reduces the stats partials in fp64.  Writes any of: fp32 stats
 // (n_k, s_k, sq_k), fp32 new parameters (M-step with the native clamps),
 // the precomputed coefficients for the next iteration (params_next/bias_next),
 // and ll_out = sum(lnsum)/N.
-hipError_t launch_reduce(const Geom& g, const float* part, const double* lnsum,
+hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s);

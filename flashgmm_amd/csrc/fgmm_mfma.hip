@@ -4,18 +4,19 @@
 //     ll2[n][k] = bias_k + sum_f P[k][f] * feat_f(x_n),
 //     feat = [x_0^2 .. x_{dp-1}^2, x_0 .. x_{dp-1}]      (2*dp features)
 // on fp64 MFMA (v_mfma_f64_16x16x4_f64), and Pass 2 accumulates
-//     S[k][f] += sum_n gamma[n][k] * [x_n, x_n^2]_f
-// on fp32 MFMA (v_mfma_f32_16x16x4_f32) straight from the accumulator
-// registers of the first product: the fp64 accumulator layout gives lane
-// (g, c) = (l/16, l%16) the values of points 4r+g (r = 0..3) for component c,
-// which is exactly the A-operand layout of the fp32 instruction when step r
-// of the stats product contracts over points {4r+g}.  No LDS transpose and no
-// N x K array.
+//     S[k][j] += sum_n gamma[n][k] * x_nj      (fp32 MFMA, fp32 accumulate)
+//     Q[k][j] += sum_n gamma[n][k] * x_nj^2    (fp64 MFMA: x^2 is exact in fp64)
+// straight from the accumulator registers of the first product: the fp64
+// accumulator layout gives lane (g, c) = (l/16, l%16) the values of points
+// 4r+g (r = 0..3) for component c, which is exactly the A-operand layout of
+// the 16x16x4 instructions when step r of the stats product contracts over
+// points {4r+g}.  No LDS transpose and no N x K array.  (x^2 rounded to fp32
+// would cost components with few, far-out members ~1e-5 in var.)
 //
 // Reference kernels these replace (file:line in the reference repository):
 //   Pass 1  flash_log_normalizer_v2_kernel    flash_gmm/csrc/flash_gmm_cuda.cu:72-170
 //   Pass 2  flash_accumulate_stats_v2_kernel  flash_gmm/csrc/flash_gmm_cuda.cu:179-292
-// Pass 2 here writes one deterministic fp32 partial per (point chunk,
+// Pass 2 here writes one deterministic fp64 partial per (point chunk,
 // component) instead of issuing global float atomics (cu:284-291).
 #include <float.h>
 #include <math.h>
@@ -154,14 +155,14 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
 // Workgroup = 4 wavefronts, each owning one 16-component subtile (its fp64
 // coefficients live in registers for the whole launch) and sharing the point
 // tiles staged in LDS.  blockIdx.y selects a chunk of points; the workgroup
-// writes one fp32 partial row [sum gamma*x | sum gamma*x^2 | sum gamma] per
+// writes one fp64 partial row [sum gamma*x | sum gamma*x^2 | sum gamma] per
 // component, reduced later in fp64 in a fixed order (no atomics).
 // ---------------------------------------------------------------------------
 template <int DP, bool VEC>
 __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const double* __restrict__ P,
     const double* __restrict__ bias, const double* __restrict__ ln2,
-    float* __restrict__ part, long chunk, int stat_w) {
+    double* __restrict__ part, long chunk, int stat_w) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int XS = DP + 20;  // LDS row stride in floats (16-byte aligned rows)
   constexpr int NFT = DP / 16;
@@ -186,13 +187,14 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     for (int s = 0; s < S1; s++) pr[s] = 0.0;
   }
 
-  f32x4 accS[NFT], accQ[NFT];
+  f32x4 accS[NFT];
+  f64x4 accQ[NFT];
 #pragma unroll
   for (int f = 0; f < NFT; f++) {
     accS[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-    accQ[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accQ[f] = f64x4{0.0, 0.0, 0.0, 0.0};
   }
-  float nk = 0.f;
+  double nk = 0.0;
 
   for (long t0 = p0; t0 < p1; t0 += kP2Tile) {
     __syncthreads();
@@ -239,30 +241,33 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
         const int pl = sub * 16 + 4 * r + g;
         const double ll = a0[r] + a1[r];
         gm[r] = (t0 + pl < p1) ? exp2f((float)(ll - ls[pl])) : 0.f;
-        nk += gm[r];
+        nk += (double)gm[r];
       }
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const float* xrow = xs + (sub * 16 + 4 * r + g) * XS + c;
+        const double g64 = (double)gm[r];
 #pragma unroll
         for (int f = 0; f < NFT; f++) {
           const float xb = xrow[f * 16];
+          const double xd = (double)xb;
           accS[f] = mfma32(gm[r], xb, accS[f]);
-          accQ[f] = mfma32(gm[r], xb * xb, accQ[f]);
+          accQ[f] = mfma64(g64, xd * xd, accQ[f]);
         }
       }
     }
   }
 
   if (!active) return;
-  float* out = part + ((size_t)blockIdx.y * Kp + (size_t)ks * 16) * stat_w;
+  double* out = part + ((size_t)blockIdx.y * Kp + (size_t)ks * 16) * stat_w;
+  // fp32 16x16x4 accumulator: register r of lane (g, c) is row 4g+r;
+  // fp64 16x16x4 accumulator: register r of lane (g, c) is row 4r+g.
 #pragma unroll
   for (int f = 0; f < NFT; f++) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int kl = 4 * g + r;
-      out[(size_t)kl * stat_w + f * 16 + c] = accS[f][r];
-      out[(size_t)kl * stat_w + DP + f * 16 + c] = accQ[f][r];
+      out[(size_t)(4 * g + r) * stat_w + f * 16 + c] = (double)accS[f][r];
+      out[(size_t)(4 * r + g) * stat_w + DP + f * 16 + c] = accQ[f][r];
     }
   }
   nk += __shfl_xor(nk, 16, 64);
@@ -292,7 +297,7 @@ static hipError_t p1_launch(const Geom& g, const float* X, const double* P,
 
 template <int DP, bool VEC>
 static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
-                            const double* bias, const double* ln2, float* part,
+                            const double* bias, const double* ln2, double* part,
                             hipStream_t s) {
   hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC>), dim3(g.p2_kblocks, g.p2_chunks),
                      dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
@@ -322,7 +327,7 @@ hipError_t launch_pass1_mfma(const Geom& g, const float* X, const double* P,
 }
 
 hipError_t launch_pass2_mfma(const Geom& g, const float* X, const double* P,
-                             const double* bias, const double* ln2, float* part,
+                             const double* bias, const double* ln2, double* part,
                              hipStream_t s) {
   const bool v = x_is_vec(X, g.d);
   switch (g.dp) {

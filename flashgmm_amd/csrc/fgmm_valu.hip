@@ -90,12 +90,12 @@ template <int DP>
 __global__ __launch_bounds__(256) void pass2_valu_kernel(
     const float* __restrict__ X, long N, int d, int K, int Kp,
     const double* __restrict__ P, const double* __restrict__ bias,
-    const double* __restrict__ ln2, float* __restrict__ part, long chunk, int stat_w) {
+    const double* __restrict__ ln2, double* __restrict__ part, long chunk, int stat_w) {
   constexpr int XS = DP + 1;
   constexpr int G = 256 / DP;  // point groups in phase B
   __shared__ float xs[kV2Tile * XS];
   __shared__ float gs[kV2Tile * kV2Comp];
-  __shared__ float red[256];
+  __shared__ double red[256];
   const int tid = threadIdx.x;
   const int k0 = blockIdx.x * kV2Comp;
   const long p0 = (long)blockIdx.y * chunk;
@@ -104,9 +104,14 @@ __global__ __launch_bounds__(256) void pass2_valu_kernel(
   const double* MS = P + (size_t)Kp * DP;
   const int j = tid % DP, grp = tid / DP;
 
-  float accS[kV2Comp], accQ[kV2Comp], accN[kV2Comp];
+  // sum gamma*x in fp32; sum gamma*x^2 and sum gamma in fp64 (x^2 exact)
+  float accS[kV2Comp];
+  double accQ[kV2Comp], accN[kV2Comp];
 #pragma unroll
-  for (int u = 0; u < kV2Comp; u++) accS[u] = accQ[u] = accN[u] = 0.f;
+  for (int u = 0; u < kV2Comp; u++) {
+    accS[u] = 0.f;
+    accQ[u] = accN[u] = 0.0;
+  }
 
   for (long t0 = p0; t0 < p1; t0 += kV2Tile) {
     __syncthreads();
@@ -139,28 +144,28 @@ __global__ __launch_bounds__(256) void pass2_valu_kernel(
     if (grp < G) {
       for (int pl = grp; pl < kV2Tile; pl += G) {
         const float xv = xs[pl * XS + j];
-        const float x2 = xv * xv;
+        const double x2 = (double)xv * (double)xv;
 #pragma unroll
         for (int u = 0; u < kV2Comp; u++) {
           const float gg = gs[pl * kV2Comp + u];
           accS[u] = fmaf(gg, xv, accS[u]);
-          accQ[u] = fmaf(gg, x2, accQ[u]);
-          accN[u] += gg;
+          accQ[u] = fma((double)gg, x2, accQ[u]);
+          accN[u] += (double)gg;
         }
       }
     }
   }
 
   // merge the G point groups (fixed order) and write the partial rows
-  float* out = part + ((size_t)blockIdx.y * Kp + k0) * stat_w;
+  double* out = part + ((size_t)blockIdx.y * Kp + k0) * stat_w;
   for (int u = 0; u < kV2Comp; u++) {
     for (int which = 0; which < 3; which++) {
-      const float v = which == 0 ? accS[u] : (which == 1 ? accQ[u] : accN[u]);
+      const double v = which == 0 ? (double)accS[u] : (which == 1 ? accQ[u] : accN[u]);
       __syncthreads();
-      red[tid] = (grp < G) ? v : 0.f;
+      red[tid] = (grp < G) ? v : 0.0;
       __syncthreads();
       if (tid < DP && k0 + u < Kp) {
-        float t = 0.f;
+        double t = 0.0;
         for (int q = 0; q < G; q++) t += red[q * DP + tid];
         if (which == 0) out[(size_t)u * stat_w + tid] = t;
         else if (which == 1) out[(size_t)u * stat_w + DP + tid] = t;
@@ -181,7 +186,7 @@ static hipError_t v1_launch(const Geom& g, const float* X, const double* P,
 
 template <int DP>
 static hipError_t v2_launch(const Geom& g, const float* X, const double* P,
-                            const double* bias, const double* ln2, float* part,
+                            const double* bias, const double* ln2, double* part,
                             hipStream_t s) {
   hipLaunchKernelGGL((pass2_valu_kernel<DP>), dim3(g.p2_kblocks, g.p2_chunks), dim3(256), 0,
                      s, X, g.N, g.d, g.K, g.Kp, P, bias, ln2, part, g.p2_chunk, g.stat_w);
@@ -202,7 +207,7 @@ hipError_t launch_pass1_valu(const Geom& g, const float* X, const double* P,
 }
 
 hipError_t launch_pass2_valu(const Geom& g, const float* X, const double* P,
-                             const double* bias, const double* ln2, float* part,
+                             const double* bias, const double* ln2, double* part,
                              hipStream_t s) {
   switch (g.dp) {
     case 16: return v2_launch<16>(g, X, P, bias, ln2, part, s);

@@ -68,9 +68,8 @@ def _params(X, mu, var, log_pi, fn):
 def _ws(X, N, K, d, variant):
     lib = _lib.load()
     nbytes = lib.fgmm_workspace_bytes(N, K, d, variant)
-    if nbytes == 0:
-        raise RuntimeError(f"flashgmm_amd: unsupported problem N={N} K={K} d={d} "
-                           f"variant={variant}")
+    if nbytes == 0:   # the library rejected the shape; report its reason
+        raise RuntimeError("flashgmm_amd: " + lib.fgmm_last_error().decode(errors="replace"))
     return _lib.workspace(X.device, nbytes), nbytes
 
 

@@ -1,0 +1,109 @@
+"""The C ABI without a GPU: the library loads, exports every symbol
+include/flashgmm.h declares, and rejects bad arguments before queuing any
+device work (these calls never reach the HIP runtime)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashgmm.h")
+LIB = os.path.join(ROOT, "flashgmm_amd", "libflashgmm.so")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fgmm_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} missing: run python -m flashgmm_amd.build")
+    from flashgmm_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for must in ("fgmm_em_fused", "fgmm_log_normalizer", "fgmm_accumulate_stats",
+                 "fgmm_m_step_update", "fgmm_em_fit", "fgmm_workspace_bytes"):
+        assert must in names
+
+
+def test_every_declared_symbol_exported(lib):
+    raw = ctypes.CDLL(LIB)
+    for name in declared():
+        assert hasattr(raw, name), f"{name} declared in flashgmm.h but not exported"
+
+
+def test_python_signatures_cover_header():
+    from flashgmm_amd import _lib
+    assert sorted(_lib.SIGNATURES) == declared()
+
+
+def test_version_and_variant_table(lib):
+    assert lib.fgmm_version() >= 100
+    # matrix cores from K >= 16 and d <= 128, vector ALU otherwise
+    assert lib.fgmm_resolve_variant(65536, 256, 128, 0) == 2
+    assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 1
+    assert lib.fgmm_resolve_variant(4096, 64, 200, 0) == 1
+    assert lib.fgmm_resolve_variant(4096, 8, 32, 2) == 2
+
+
+def test_workspace_bytes(lib):
+    for N, K, d in ((4096, 8, 32), (65536, 256, 128), (1048576, 512, 128), (1, 1, 1), (5, 3, 256)):
+        for v in (0, 1, 2):
+            if v == 2 and d > 128:
+                assert lib.fgmm_workspace_bytes(N, K, d, v) == 0
+                continue
+            b = lib.fgmm_workspace_bytes(N, K, d, v)
+            assert b > 0 and b % 256 == 0
+            assert b >= 8 * N      # holds the fp64 log-normalizer at least
+    assert lib.fgmm_workspace_bytes(0, 8, 32, 0) == 0
+    assert lib.fgmm_workspace_bytes(10, 8, 257, 0) == 0
+
+
+def _em(lib, N=100, K=4, d=8, variant=0, ws=0x1000, wsb=1 << 30, null=None):
+    p = [0x1000] * 8
+    if null is not None:
+        p[null] = None
+    return lib.fgmm_em_fused(p[0], p[1], p[2], p[3], N, K, d, variant, p[4], p[5], p[6], p[7],
+                             ws, wsb, None)
+
+
+def test_argument_errors_before_device_work(lib):
+    assert _em(lib, N=0) == 1 and b"N must be" in lib.fgmm_last_error()
+    assert _em(lib, K=0) == 1 and b"K must be" in lib.fgmm_last_error()
+    assert _em(lib, d=0) == 1 and b"d must be" in lib.fgmm_last_error()
+    assert _em(lib, d=257) == 1 and b"d must be" in lib.fgmm_last_error()
+    assert _em(lib, d=200, variant=2) == 1 and b"MFMA" in lib.fgmm_last_error()
+    assert _em(lib, variant=7) == 1 and b"variant" in lib.fgmm_last_error()
+    for i in range(8):
+        assert _em(lib, null=i) == 1 and b"must not be NULL" in lib.fgmm_last_error()
+    assert _em(lib, ws=None) == 2 and b"NULL" in lib.fgmm_last_error()
+    assert _em(lib, ws=0x1001) == 2 and b"aligned" in lib.fgmm_last_error()
+    assert _em(lib, wsb=16) == 2 and b"too small" in lib.fgmm_last_error()
+    assert lib.fgmm_em_fit(1, 1, 1, 1, 100, 4, 8, 0, 0, 1, 1, 1, 1, 0x1000, 1 << 30, None) == 1
+    assert b"iters" in lib.fgmm_last_error()
+    assert lib.fgmm_m_step_update(None, 1, 1, 10, 4, 8, 1, 1, 1, None) == 1
+
+
+def test_python_errors_mirror_reference():
+    import torch
+    from flashgmm_amd import flash_gmm_native as C
+    X = torch.zeros(10, 4)
+    mu, var, lp = torch.zeros(2, 4), torch.ones(2, 4), torch.zeros(2)
+    with pytest.raises(RuntimeError, match="X must be float32"):
+        C.flash_em_fused(X.double(), mu, var, lp)
+    with pytest.raises(RuntimeError, match="X must be 2D"):
+        C.flash_log_normalizer(X[0], mu, var, lp)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        C.flash_em_fused(X, mu, var, lp)
+    with pytest.raises(RuntimeError, match="BN and BK"):
+        C.flash_em_fused(X, mu, var, lp, 0, 8)
+    with pytest.raises(RuntimeError, match="unknown variant"):
+        from flashgmm_amd import _lib
+        _lib.variant_code("fast")

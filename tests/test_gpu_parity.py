@@ -1,0 +1,305 @@
+"""GPU parity: the HIP path (through the C ABI) against the fp64 oracle.
+
+Tolerances (the benchmark's parity bar, checked against the fp64 oracle):
+  * log_normalizer: relative error <= 1e-5;
+  * mu, var after one iteration: |gpu - fp64| <= max(1e-5, 2 ulp_fp32(value))
+    -- the ulp floor only matters for |value| >= 64, where 1e-5 is below the
+    resolution of the fp32 outputs themselves;
+  * pi = exp(log_pi): |gpu - fp64| <= 1e-5;
+  * mean log-likelihood trajectory over 20 iterations: relative <= 1e-4.
+The reference's own fp32 arithmetic (oracle c32_*, bit-identical to its C++
+CPU path) misses the 1e-5 bar at the headline shape; a test below records
+that the GPU path is closer to the fp64 truth than the reference is.
+"""
+import functools
+
+import numpy as np
+import pytest
+
+from flashgmm_amd.configs import CONFIGS, make_problem
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(1, None), (2, None), (3, None), (4, None), (5, 131072)]
+
+
+def ulp32(x):
+    return np.spacing(np.abs(np.asarray(x, np.float64)).astype(np.float32)).astype(np.float64)
+
+
+def check_params(got, ref64, label):
+    g_mu, g_var, g_lp = (np.asarray(a, np.float64) for a in got)
+    r_mu, r_var, r_lp = (np.asarray(a, np.float64) for a in ref64)
+    for name, g, r in (("mu", g_mu, r_mu), ("var", g_var, r_var)):
+        err = np.abs(g - r)
+        tol = np.maximum(1e-5, 2 * ulp32(r))
+        ratio = err / tol
+        i = int(ratio.argmax())
+        assert ratio.flat[i] <= 1.0, (f"{label}: {name} err {err.flat[i]:.3e} > tol "
+                                      f"{tol.flat[i]:.3e} at {np.unravel_index(i, err.shape)} "
+                                      f"(value {r.flat[i]:.6g}; max err {err.max():.3e})")
+    epi = np.abs(np.exp(g_lp) - np.exp(r_lp)).max()
+    assert epi <= 1e-5, f"{label}: pi max err {epi:.3e}"
+
+
+def check_ln(got, ref, label, tol=1e-5):
+    e = np.max(np.abs(np.asarray(got, np.float64) - ref) / np.abs(ref))
+    assert e <= tol, f"{label}: log_normalizer max rel err {e:.3e}"
+
+
+@functools.lru_cache(maxsize=None)
+def problem(cid, N):
+    return make_problem(cid, N)
+
+
+@functools.lru_cache(maxsize=None)
+def oracle_iter(cid, N):
+    X, mu, var, lp = problem(cid, N)
+    _, _, _, ln, (n_k, s_k, sq_k) = O.c_em_fused(X, mu, var, lp, with_stats=True)
+    m64, v64, l64 = O.c_m_step_update(n_k, s_k, sq_k, X.shape[0])
+    return m64, v64, l64, ln, n_k, s_k, sq_k
+
+
+def to_dev(cuda, *arrs):
+    import torch
+    return [torch.from_numpy(np.ascontiguousarray(a)).to(cuda) for a in arrs]
+
+
+def variants_for(K, d):
+    v = ["valu"]
+    if d <= 128:
+        v.append("mfma")
+    return v
+
+
+@pytest.mark.parametrize("cid,N", CASES, ids=[f"C{c}" + (f"_N{n}" if n else "") for c, n in CASES])
+def test_em_fused_matches_oracle(cuda, cid, N):
+    from flashgmm_amd import flash_gmm_native as C
+    X, mu, var, lp = problem(cid, N)
+    m64, v64, l64, ln, *_ = oracle_iter(cid, N)
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in variants_for(mu.shape[0], mu.shape[1]):
+        print(f"[case] em_fused C{cid} N={X.shape[0]} variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
+        check_params(out[:3], (m64, v64, l64), f"C{cid} {variant}")
+        check_ln(out[3], ln, f"C{cid} {variant}")
+
+
+@pytest.mark.parametrize("cid,N", [(1, None), (2, 16384), (4, 8192)])
+def test_stage_entry_points(cuda, cid, N):
+    from flashgmm_amd import flash_gmm_native as C
+    X, mu, var, lp = problem(cid, N)
+    _, _, _, ln, n_k, s_k, sq_k = oracle_iter(cid, N)
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in variants_for(mu.shape[0], mu.shape[1]):
+        print(f"[case] stages C{cid} N={X.shape[0]} variant={variant}", flush=True)
+        g_ln = C.flash_log_normalizer(*t, variant=variant)
+        check_ln(g_ln.cpu().numpy(), ln, f"pass1 C{cid} {variant}")
+        g_nk, g_sk, g_sqk = C.flash_accumulate_stats(*t, g_ln, variant=variant)
+        for name, g, r in (("n_k", g_nk, n_k), ("s_k", g_sk, s_k), ("sq_k", g_sqk, sq_k)):
+            g = g.cpu().numpy().astype(np.float64)
+            e = np.abs(g - r).max() / max(1.0, np.abs(r).max())
+            assert e <= 1e-5, f"pass2 C{cid} {variant}: {name} normwise err {e:.3e}"
+        assert abs(g_nk.double().sum().item() - X.shape[0]) <= 1e-5 * X.shape[0]
+        mu2, var2, lp2 = C.m_step_update(g_nk, g_sk, g_sqk, X.shape[0])
+        ref = O.c_m_step_update(g_nk.cpu().numpy(), g_sk.cpu().numpy(), g_sqk.cpu().numpy(),
+                                X.shape[0])
+        for g, r in zip((mu2, var2, lp2), ref):
+            e = np.abs(g.cpu().numpy().astype(np.float64) - r)
+            assert np.all(e <= np.maximum(2 * ulp32(r), 1e-12)), "m_step_update rounding"
+
+
+@pytest.mark.parametrize("name", ["k1_d3", "k4_d8", "c1_head512", "overlap_k6_d5",
+                                  "empty_component", "ragged_k17_d33"])
+def test_golden_vectors(cuda, name):
+    import os
+    from flashgmm_amd import flash_gmm_native as C
+    path = os.path.join(os.path.dirname(__file__), "golden", f"{name}.npz")
+    with np.load(path, allow_pickle=False) as z:
+        g = {k: z[k] for k in z.files}
+    t = to_dev(cuda, g["X"], g["mu"], g["var"], g["log_pi"])
+    for variant in ("valu", "mfma"):
+        print(f"[case] golden {name} variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
+        check_ln(out[3], g["ln"], f"{name} {variant}")
+        check_params(out[:3], (g["new_mu"], g["new_var"], g["new_log_pi"]), f"{name} {variant}")
+
+
+def _traj_fixture():
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "trajectories.json")
+    return json.load(open(path)) if os.path.exists(path) else {}
+
+
+@pytest.mark.parametrize("cid", sorted(CONFIGS))
+def test_ll_trajectory_full_size(cuda, cid):
+    """Full benchmark size against the fp64 oracle trajectories stored in
+    tests/golden/trajectories.json (written by make_trajectories.py)."""
+    from flashgmm_amd import flash_gmm_native as C
+    ref = _traj_fixture().get(f"C{cid}")
+    if ref is None:
+        pytest.skip(f"no stored trajectory for C{cid}")
+    X, mu, var, lp = problem(cid, None)
+    assert (ref["N"], ref["K"], ref["d"]) == X.shape[:1] + mu.shape
+    t = to_dev(cuda, X, mu, var, lp)
+    traj_ref = np.array(ref["ll"])
+    for variant in variants_for(mu.shape[0], mu.shape[1]):
+        print(f"[case] full trajectory C{cid} iters={ref['iters']} variant={variant}", flush=True)
+        _, _, _, traj = C.em_fit(*t, ref["iters"], variant=variant)
+        e = np.abs(traj.cpu().numpy() - traj_ref) / np.abs(traj_ref)
+        assert e.max() <= 1e-4, f"C{cid} {variant}: trajectory rel err {e.max():.3e} at it {e.argmax()}"
+
+
+# Reduced-size trajectories against the live oracle.  C4 is not reduced: at
+# 8 points per component its 20-step trajectory is ill-conditioned enough that
+# one-ulp parameter differences grow past 1e-4; it is covered at full size.
+@pytest.mark.parametrize("cid,N,iters", [(1, None, 20), (2, 16384, 20), (3, 32768, 20),
+                                         (5, 32768, 10)])
+def test_ll_trajectory(cuda, cid, N, iters):
+    from flashgmm_amd import flash_gmm_native as C
+    X, mu, var, lp = problem(cid, N)
+    traj_ref, m_ref, v_ref, l_ref = O.c_fit(X, mu, var, lp, iters)
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in variants_for(mu.shape[0], mu.shape[1]):
+        print(f"[case] trajectory C{cid} N={X.shape[0]} iters={iters} variant={variant}", flush=True)
+        _, _, _, traj = C.em_fit(*t, iters, variant=variant)
+        traj = traj.cpu().numpy()
+        e = np.abs(traj - traj_ref) / np.abs(traj_ref)
+        assert e.max() <= 1e-4, f"C{cid} {variant}: trajectory rel err {e.max():.3e} at it {e.argmax()}"
+
+
+def test_driver_matches_device_loop(cuda):
+    """NativeFlashGMM.fit (per-call path, host sync per iteration) and
+    fit_device (one device loop) record the same history."""
+    import torch
+    from flashgmm_amd.native_wrapper import NativeFlashGMM
+    X, *_ = problem(1, None)
+    Xd = torch.from_numpy(X).to(cuda)
+    h1 = NativeFlashGMM(K=8, d=32, max_iter=10, tol=0.0).fit(Xd)
+    h2 = NativeFlashGMM(K=8, d=32, max_iter=10, tol=0.0).fit_device(Xd)
+    assert [h["iter"] for h in h1] == [h["iter"] for h in h2] == list(range(10))
+    for a, b in zip(h1, h2):
+        assert abs(a["log_likelihood"] - b["log_likelihood"]) <= 1e-6 * abs(b["log_likelihood"])
+    # early stop follows the reference rule |dLL| < tol
+    h3 = NativeFlashGMM(K=8, d=32, max_iter=100, tol=1e-4).fit(Xd)
+    assert len(h3) < 100 and abs(h3[-1]["log_likelihood"] - h3[-2]["log_likelihood"]) < 1e-4
+
+
+def test_more_accurate_than_reference_fp32(cuda):
+    """At the headline shape the reference's fp32 arithmetic sits ~1e-4 from
+    the fp64 truth; the GPU path must be at least as close."""
+    from flashgmm_amd import flash_gmm_native as C
+    X, mu, var, lp = problem(2, None)
+    m64, v64, l64, ln, *_ = oracle_iter(2, None)
+    r_mu, r_var, r_lp, r_ln = O.c32_em_fused(X, mu, var, lp)
+    g = [o.cpu().numpy() for o in C.flash_em_fused(*to_dev(cuda, X, mu, var, lp))]
+    for gi, ri, ti in ((g[0], r_mu, m64), (g[1], r_var, v64)):
+        assert np.abs(gi - ti).max() <= np.abs(ri - ti).max()
+    print(f"[info] C2 max|var err|: gpu {np.abs(g[1]-v64).max():.2e}  "
+          f"reference fp32 {np.abs(r_var-v64).max():.2e}")
+
+
+def test_full_size_properties(cuda):
+    """C5 at its full size (1M points): properties that need no oracle."""
+    import torch
+    from flashgmm_amd import flash_gmm_native as C
+    X, mu, var, lp = problem(5, None)
+    t = to_dev(cuda, X, mu, var, lp)
+    print("[case] C5 full-size properties", flush=True)
+    a = C.flash_em_fused(*t)
+    b = C.flash_em_fused(*t)
+    for x, y in zip(a, b):                                  # bitwise repeatable (no atomics)
+        assert torch.equal(x, y)
+    ln = a[3]
+    assert torch.isfinite(ln).all()
+    n_k, s_k, sq_k = C.flash_accumulate_stats(*t, ln)
+    assert abs(n_k.double().sum().item() - X.shape[0]) <= 1e-5 * X.shape[0]
+    # ln of a row does not depend on the other rows: permuting X permutes ln
+    p = torch.from_numpy(np.random.default_rng(0).permutation(X.shape[0])).to(cuda)
+    ln_p = C.flash_log_normalizer(t[0][p].contiguous(), *t[1:])
+    assert torch.equal(ln_p, ln[p])
+    # statistics are additive over point chunks
+    h = X.shape[0] // 2
+    s1 = C.flash_accumulate_stats(t[0][:h].contiguous(), *t[1:], ln[:h].contiguous())
+    s2 = C.flash_accumulate_stats(t[0][h:].contiguous(), *t[1:], ln[h:].contiguous())
+    for whole, u, v in zip((n_k, s_k, sq_k), s1, s2):
+        e = (whole.double() - u.double() - v.double()).abs().max().item()
+        assert e <= 1e-5 * max(1.0, whole.double().abs().max().item())
+
+
+EDGE = {
+    "N1": dict(N=1, K=3, d=5),
+    "K1": dict(N=300, K=1, d=7),
+    "d1": dict(N=257, K=4, d=1),
+    "d33_K17": dict(N=1000, K=17, d=33),
+    "d256": dict(N=300, K=5, d=256),
+    "d130": dict(N=100, K=20, d=130),
+    "K33_N1025": dict(N=1025, K=33, d=64),
+}
+
+
+@pytest.mark.parametrize("name", sorted(EDGE))
+def test_edge_shapes(cuda, name):
+    from flashgmm_amd import flash_gmm_native as C
+    cfg = EDGE[name]
+    rng = np.random.default_rng(11)
+    N, K, d = cfg["N"], cfg["K"], cfg["d"]
+    X = (rng.uniform(-4, 4, (K, d))[rng.integers(0, K, N)] + rng.normal(0, 1, (N, d))).astype(np.float32)
+    mu = X[rng.choice(N, K, replace=N < K)].copy() if N >= 1 else None
+    mu = (mu + rng.normal(0, 0.1, mu.shape)).astype(np.float32)
+    var = rng.uniform(0.5, 2.0, (K, d)).astype(np.float32)
+    lp = np.log(rng.dirichlet(np.ones(K))).astype(np.float32)
+    ref = O.np_em_fused(X, mu, var, lp)
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in variants_for(K, d):
+        print(f"[case] edge {name} variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
+        check_ln(out[3], ref[3], f"{name} {variant}")
+        check_params(out[:3], ref[:3], f"{name} {variant}")
+
+
+def test_unaligned_and_noncontiguous_inputs(cuda):
+    import torch
+    from flashgmm_amd import flash_gmm_native as C
+    X, mu, var, lp = problem(1, None)
+    ref = oracle_iter(1, None)
+    big = torch.zeros(X.size + 1, dtype=torch.float32, device=cuda)
+    big[1:] = torch.from_numpy(X.ravel()).to(cuda)
+    Xu = big[1:].view(X.shape)                    # 4-byte offset: scalar load path
+    assert Xu.data_ptr() % 16 != 0
+    t = to_dev(cuda, mu, var, lp)
+    for variant in ("valu", "mfma"):
+        print(f"[case] unaligned X variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(Xu, *t, variant=variant)]
+        check_params(out[:3], ref[:3], f"unaligned {variant}")
+    Xt = torch.from_numpy(np.ascontiguousarray(X.T)).to(cuda).t()   # non-contiguous view
+    out = [o.cpu().numpy() for o in C.flash_em_fused(Xt, *t)]
+    check_params(out[:3], ref[:3], "transposed view")
+
+
+def test_shape_errors_raise_before_launch(cuda):
+    import torch
+    from flashgmm_amd import flash_gmm_native as C
+    X = torch.zeros(64, 8, device=cuda)
+    mu, var, lp = torch.zeros(4, 8, device=cuda), torch.ones(4, 8, device=cuda), torch.zeros(4, device=cuda)
+    with pytest.raises(RuntimeError, match="var must be"):
+        C.flash_em_fused(X, mu, var[:, :4], lp)
+    with pytest.raises(RuntimeError, match="log_pi must be"):
+        C.flash_em_fused(X, mu, var, lp[:3])
+    with pytest.raises(RuntimeError, match="d must be <= 256"):
+        C.flash_em_fused(torch.zeros(4, 300, device=cuda), torch.zeros(2, 300, device=cuda),
+                         torch.ones(2, 300, device=cuda), torch.zeros(2, device=cuda))
+    with pytest.raises(RuntimeError, match="is on cpu"):
+        C.flash_em_fused(X, mu.cpu(), var, lp)
+    with pytest.raises(RuntimeError, match="MFMA variant supports d <= 128"):
+        C.flash_em_fused(torch.zeros(4, 200, device=cuda), torch.zeros(2, 200, device=cuda),
+                         torch.ones(2, 200, device=cuda), torch.zeros(2, device=cuda),
+                         variant="mfma")
+
+
+def test_native_library_is_what_ran(cuda):
+    from flashgmm_amd import _lib
+    maps = open("/proc/self/maps").read()
+    assert _lib.LIB_PATH in maps
