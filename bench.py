@@ -161,6 +161,19 @@ def cpu_baseline(cid, budget_s):
                       f"{per*1000:.1f} ms each"}
 
 
+def measured_traffic(cid):
+    """HBM bytes per Pass-2 launch from the committed rocprofv3 counter runs
+    (profiles/hbm_traffic.json), or None when that workload was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        rec = json.load(open(path)).get(f"C{cid}")
+    except (OSError, ValueError):
+        return None
+    if not rec:
+        return None
+    return rec["read_bytes"] + rec["write_bytes"]
+
+
 def line_for(cid, args, with_cpu):
     cfg = CONFIGS[cid]
     r = run_gpu(cid, args.steps, args.warmup, args.variant)
@@ -192,7 +205,8 @@ def line_for(cid, args, with_cpu):
             "peak": FP32_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / FP32_PEAK,
-            "traffic": None,
+            "traffic": measured_traffic(cid),
+            "traffic_unit": "bytes/launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE, profiles/)",
             "peak_at_kernel_precision": pass2_peak() / 1e12,
             "frac_at_kernel_precision": achieved / pass2_peak(),
         },

@@ -65,11 +65,13 @@ Geom make_geom(long N, int K, int d, int variant) {
   }
   // Pass 2 splits the points into S chunks so that ~512 workgroups (two per
   // CU) are in flight; each chunk leaves one fp64 partial row per component.
-  // Chunks stay <= 4096 points so the fp32 sum of gamma*x stays short.
+  // Chunks stay <= 16384 points, which bounds the fp32 sum of gamma*x
+  // (its rounding moves mu by ~1e-6 at that length; sums of gamma*x^2 and
+  // gamma are fp64).
   const long tile = 64;
   long tiles = (N + tile - 1) / tile;
   long S = (512 + g.p2_kblocks - 1) / g.p2_kblocks;
-  if (S < (N + 4095) / 4096) S = (N + 4095) / 4096;
+  if (S < (N + 16383) / 16384) S = (N + 16383) / 16384;
   if (S > tiles) S = tiles;
   if (S < 1) S = 1;
   long chunk = round_up_l((N + S - 1) / S, tile);

@@ -25,11 +25,13 @@
 
 namespace fgmm {
 
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kP1Waves = 8;            // Pass 1: wavefronts per workgroup
 constexpr int kP1Points = 16 * kP1Waves;
+constexpr int kP1Threads = 64 * kP1Waves;
 constexpr int kP1Sub = 2;              // 16-component subtiles per LDS tile
 constexpr int kP2Waves = 4;            // Pass 2: one 16-component subtile each
 constexpr int kP2Tile = 64;            // Pass 2: points per LDS tile
@@ -61,13 +63,17 @@ __device__ inline void load_quarter(const float* __restrict__ X, long n, long N,
   }
 }
 
+
 // ---------------------------------------------------------------------------
 // Pass 1: log-normalizer.  Workgroup = 8 wavefronts x 16 points; each lane
 // keeps the quarter of its point's features it feeds to the B operand in
-// registers for the whole sweep over K, which streams through LDS in tiles of
-// 32 components (fragment-ordered fp64 coefficients, one contiguous copy).
-// Each lane runs an online (max, sum) over the 4 components per subtile its
-// accumulator rows hold; the four lane groups merge at the end.
+// registers for the whole sweep over K.  The coefficients stream through two
+// LDS buffers in tiles of 32 components (one contiguous fragment-ordered
+// copy each): while the wavefronts run the MFMAs of tile t, every thread
+// holds its share of tile t+1 in registers and stores it to the other buffer
+// afterwards, so one barrier per tile separates the stages.  Each lane runs
+// an online (max, sum) over the 4 components per subtile its accumulator
+// rows hold; the four lane groups merge at the end.
 // ---------------------------------------------------------------------------
 template <int DP, bool VEC>
 __global__ __launch_bounds__(512) void pass1_mfma_kernel(
@@ -75,10 +81,10 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
     const double* __restrict__ bias, double* __restrict__ ln2,
     float* __restrict__ ln_out, double* __restrict__ lnsum) {
   constexpr int Q = DP / 4, S1 = DP / 2;
-  constexpr int TILE = kP1Sub * S1 * 64;  // doubles per K tile
-  extern __shared__ double smem[];
-  double* sP = smem;
-  __shared__ double sB[16 * kP1Sub];
+  constexpr int TILE = kP1Sub * S1 * 64;        // doubles per K tile
+  constexpr int PER = TILE / 2 / kP1Threads;    // double2 per thread per tile
+  extern __shared__ double smem[];              // [2][TILE]
+  __shared__ double sB[2][16 * kP1Sub];
   __shared__ double red[kP1Waves];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -88,21 +94,39 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
   float xq[Q];
   load_quarter<Q, VEC>(X, n, N, d, g * Q, xq);
 
-  double m = -DBL_MAX, ssum = 0.0;
   const int ntiles = Kp / (16 * kP1Sub);
-  for (int t = 0; t < ntiles; t++) {
-    __syncthreads();
-    const double2* src = reinterpret_cast<const double2*>(P + (size_t)t * TILE);
-    double2* dst = reinterpret_cast<double2*>(sP);
-    for (int i = tid; i < TILE / 2; i += blockDim.x) dst[i] = src[i];
-    if (tid < 16 * kP1Sub) sB[tid] = bias[t * 16 * kP1Sub + tid];
-    __syncthreads();
+  // staging registers for the next coefficient tile (clang vector type so
+  // the array is promoted to registers)
+  f64x2 pre[PER];
+  double preB = 0.0;
+#define FGMM_P1_GLOAD(t)                                                          \
+  {                                                                               \
+    const f64x2* src_ = reinterpret_cast<const f64x2*>(P + (size_t)(t) * TILE);   \
+    _Pragma("unroll") for (int i_ = 0; i_ < PER; i_++) pre[i_] =                   \
+        src_[tid + i_ * kP1Threads];                                              \
+    if (tid < 16 * kP1Sub) preB = bias[(t) * 16 * kP1Sub + tid];                   \
+  }
+#define FGMM_P1_LSTORE(buf)                                                       \
+  {                                                                               \
+    f64x2* dst_ = reinterpret_cast<f64x2*>(smem + (buf) * TILE);                  \
+    _Pragma("unroll") for (int i_ = 0; i_ < PER; i_++) dst_[tid + i_ * kP1Threads] = \
+        pre[i_];                                                                  \
+    if (tid < 16 * kP1Sub) sB[(buf)][tid] = preB;                                 \
+  }
+  FGMM_P1_GLOAD(0)
+  FGMM_P1_LSTORE(0)
+  __syncthreads();
 
+  double m = -DBL_MAX, ssum = 0.0;
+  for (int t = 0; t < ntiles; t++) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) FGMM_P1_GLOAD(t + 1)
+    const double* sP = smem + buf * TILE;
     f64x4 acc0, acc1;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      acc0[r] = sB[4 * r + g];
-      acc1[r] = sB[16 + 4 * r + g];
+      acc0[r] = sB[buf][4 * r + g];
+      acc1[r] = sB[buf][16 + 4 * r + g];
     }
 #pragma unroll
     for (int s = 0; s < S1; s++) {
@@ -121,7 +145,11 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
       add += (double)exp2f((float)(acc0[r] - mn)) + (double)exp2f((float)(acc1[r] - mn));
     ssum = ssum * (double)exp2f((float)(m - mn)) + add;
     m = mn;
+    if (t + 1 < ntiles) FGMM_P1_LSTORE(buf ^ 1)
+    __syncthreads();
   }
+#undef FGMM_P1_GLOAD
+#undef FGMM_P1_LSTORE
   // merge the four lane groups holding the same point
 #pragma unroll
   for (int off = 16; off <= 32; off <<= 1) {
@@ -153,27 +181,42 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
 // ---------------------------------------------------------------------------
 // Pass 2: responsibilities recomputed on chip + sufficient statistics.
 // Workgroup = 4 wavefronts, each owning one 16-component subtile (its fp64
-// coefficients live in registers for the whole launch) and sharing the point
-// tiles staged in LDS.  blockIdx.y selects a chunk of points; the workgroup
-// writes one fp64 partial row [sum gamma*x | sum gamma*x^2 | sum gamma] per
-// component, reduced later in fp64 in a fixed order (no atomics).
+// coefficients live in registers for the whole launch) and sharing 64-point
+// tiles staged in two LDS buffers (the next tile is fetched into registers
+// while the current one is consumed).  Within a tile the distance product of
+// subtile i+1 is interleaved with the statistics products of subtile i, so
+// the matrix pipe has independent work while gamma is being formed.
+//
+// The 1-D grid is mapped XCD-aware: workgroups w and w+8 run on the same XCD,
+// so the ceil(Kp/64) workgroups that read the same point chunk are given
+// linear ids of one residue class mod 8 and share that XCD's L2.
+// Each workgroup writes one fp64 partial row [sum gamma*x | sum gamma*x^2 |
+// sum gamma] per component, reduced later in fp64 in a fixed order.
 // ---------------------------------------------------------------------------
 template <int DP, bool VEC>
 __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const double* __restrict__ P,
     const double* __restrict__ bias, const double* __restrict__ ln2,
-    double* __restrict__ part, long chunk, int stat_w) {
+    double* __restrict__ part, long chunk, int nchunks, int kblocks, int stat_w) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int XS = DP + 20;  // LDS row stride in floats (16-byte aligned rows)
   constexpr int NFT = DP / 16;
-  __shared__ float xs[kP2Tile * XS];
-  __shared__ double ls[kP2Tile];
+  constexpr int V4 = kP2Tile * (DP / 4) / 256;  // float4 per thread per tile
+  __shared__ float xs[2][kP2Tile * XS];
+  __shared__ double ls[2][kP2Tile];
+
+  // XCD-aware decode of the linear workgroup id
+  const int w = blockIdx.x;
+  const int xcd = w & 7, local = w >> 3;
+  const int kb = local % kblocks;
+  const int chunk_id = (local / kblocks) * 8 + xcd;
+  if (chunk_id >= nchunks) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int ks = blockIdx.x * kP2Waves + wave;
+  const int ks = kb * kP2Waves + wave;
   const bool active = ks < (Kp >> 4);
-  const long p0 = (long)blockIdx.y * chunk;
+  const long p0 = (long)chunk_id * chunk;
   const long p1 = (p0 + chunk < N) ? p0 + chunk : N;
 
   double pr[S1];
@@ -196,10 +239,13 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
   }
   double nk = 0.0;
 
-  for (long t0 = p0; t0 < p1; t0 += kP2Tile) {
-    __syncthreads();
-    for (int i = tid; i < kP2Tile * (DP / 4); i += blockDim.x) {
-      const int row = i / (DP / 4), j = 4 * (i - row * (DP / 4));
+  float4 pre[V4];
+  double preL = 0.0;
+  auto gload = [&](long t0) {
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+      const int idx = tid + i * 256;
+      const int row = idx / (DP / 4), j = 4 * (idx - row * (DP / 4));
       const long nn = t0 + row;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (nn < p1) {
@@ -213,53 +259,90 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
           if (j + 3 < d) v.w = src[3];
         }
       }
-      *reinterpret_cast<float4*>(xs + row * XS + j) = v;
+      pre[i] = v;
     }
-    if (tid < kP2Tile) ls[tid] = (t0 + tid < p1) ? ln2[t0 + tid] : 0.0;
-    __syncthreads();
-    if (!active) continue;
+    if (tid < kP2Tile) preL = (t0 + tid < p1) ? ln2[t0 + tid] : 0.0;
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+      const int idx = tid + i * 256;
+      const int row = idx / (DP / 4), j = 4 * (idx - row * (DP / 4));
+      *reinterpret_cast<float4*>(&xs[buf][row * XS + j]) = pre[i];
+    }
+    if (tid < kP2Tile) ls[buf][tid] = preL;
+  };
 
-#pragma unroll 1
-    for (int sub = 0; sub < kP2Tile / 16; sub++) {
-      const float* xr = xs + (sub * 16 + c) * XS + g * Q;
-      f64x4 a0 = f64x4{bk, bk, bk, bk};
-      f64x4 a1 = f64x4{0.0, 0.0, 0.0, 0.0};
+  // distance product for one 16-point subtile: a0 (x^2 terms, with the
+  // bias folded in) and a1 (x terms), fp64
+  auto gemm1_block = [&](const float* xr, int s4, f64x4& a0, f64x4& a1) {
+    const float4 x4 = *reinterpret_cast<const float4*>(xr + 4 * s4);
+    const float xv4[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
-      for (int s4 = 0; s4 < Q / 4; s4++) {
-        const float4 x4 = *reinterpret_cast<const float4*>(xr + 4 * s4);
-        const float xv4[4] = {x4.x, x4.y, x4.z, x4.w};
+    for (int u = 0; u < 4; u++) {
+      const double xv = (double)xv4[u];
+      a0 = mfma64(xv * xv, pr[4 * s4 + u], a0);
+      a1 = mfma64(xv, pr[Q + 4 * s4 + u], a1);
+    }
+  };
+  // statistics products for pair p = (r, f): points 4r+g of the subtile
+  auto gemm2_pair = [&](const float* xsub, const float (&gm)[4], int p) {
+    const int r = p / NFT, f = p - r * NFT;
+    const float xb = xsub[(4 * r + g) * XS + f * 16 + c];
+    const double xd = (double)xb;
+    accS[f] = mfma32(gm[r], xb, accS[f]);
+    accQ[f] = mfma64((double)gm[r], xd * xd, accQ[f]);
+  };
+
+  const long ntile = (p1 > p0) ? (p1 - p0 + kP2Tile - 1) / kP2Tile : 0;
+  if (ntile > 0) {
+    gload(p0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (long it = 0; it < ntile; it++) {
+    const int buf = (int)(it & 1);
+    const long t0 = p0 + it * kP2Tile;
+    if (it + 1 < ntile) gload(t0 + kP2Tile);
+    if (active) {
+      const float* xt = xs[buf];
+      f64x4 a0 = f64x4{bk, bk, bk, bk}, a1 = f64x4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const double xv = (double)xv4[u];
-          a0 = mfma64(xv * xv, pr[4 * s4 + u], a0);
-          a1 = mfma64(xv, pr[Q + 4 * s4 + u], a1);
+      for (int s4 = 0; s4 < Q / 4; s4++) gemm1_block(xt + c * XS + g * Q, s4, a0, a1);
+#pragma unroll
+      for (int sub = 0; sub < kP2Tile / 16; sub++) {
+        float gm[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int pl = sub * 16 + 4 * r + g;
+          const double ll = a0[r] + a1[r];
+          gm[r] = (t0 + pl < p1) ? exp2f((float)(ll - ls[buf][pl])) : 0.f;
+          nk += (double)gm[r];
         }
-      }
-      float gm[4];
+        const float* xsub = xt + sub * 16 * XS;
+        if (sub + 1 < kP2Tile / 16) {
+          const float* xr = xt + ((sub + 1) * 16 + c) * XS + g * Q;
+          f64x4 b0 = f64x4{bk, bk, bk, bk}, b1 = f64x4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int pl = sub * 16 + 4 * r + g;
-        const double ll = a0[r] + a1[r];
-        gm[r] = (t0 + pl < p1) ? exp2f((float)(ll - ls[pl])) : 0.f;
-        nk += (double)gm[r];
-      }
+          for (int s4 = 0; s4 < Q / 4; s4++) {
+            gemm1_block(xr, s4, b0, b1);
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float* xrow = xs + (sub * 16 + 4 * r + g) * XS + c;
-        const double g64 = (double)gm[r];
+            for (int u = 0; u < 4; u++) gemm2_pair(xsub, gm, 4 * s4 + u);
+          }
+          a0 = b0;
+          a1 = b1;
+        } else {
 #pragma unroll
-        for (int f = 0; f < NFT; f++) {
-          const float xb = xrow[f * 16];
-          const double xd = (double)xb;
-          accS[f] = mfma32(gm[r], xb, accS[f]);
-          accQ[f] = mfma64(g64, xd * xd, accQ[f]);
+          for (int p = 0; p < 4 * NFT; p++) gemm2_pair(xsub, gm, p);
         }
       }
     }
+    if (it + 1 < ntile) lstore(buf ^ 1);
+    __syncthreads();
   }
 
   if (!active) return;
-  double* out = part + ((size_t)blockIdx.y * Kp + (size_t)ks * 16) * stat_w;
+  double* out = part + ((size_t)chunk_id * Kp + (size_t)ks * 16) * stat_w;
   // fp32 16x16x4 accumulator: register r of lane (g, c) is row 4g+r;
   // fp64 16x16x4 accumulator: register r of lane (g, c) is row 4r+g.
 #pragma unroll
@@ -282,7 +365,7 @@ template <int DP, bool VEC>
 static hipError_t p1_launch(const Geom& g, const float* X, const double* P,
                             const double* bias, double* ln2, float* ln_out,
                             double* lnsum, hipStream_t s) {
-  constexpr size_t lds = (size_t)kP1Sub * (DP / 2) * 64 * sizeof(double);
+  constexpr size_t lds = 2 * (size_t)kP1Sub * (DP / 2) * 64 * sizeof(double);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)pass1_mfma_kernel<DP, VEC>,
@@ -290,8 +373,8 @@ static hipError_t p1_launch(const Geom& g, const float* X, const double* P,
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((pass1_mfma_kernel<DP, VEC>), dim3(g.p1_blocks), dim3(kP1Points * 4),
-                     lds, s, X, g.N, g.d, g.Kp, P, bias, ln2, ln_out, lnsum);
+  hipLaunchKernelGGL((pass1_mfma_kernel<DP, VEC>), dim3(g.p1_blocks), dim3(kP1Threads), lds, s,
+                     X, g.N, g.d, g.Kp, P, bias, ln2, ln_out, lnsum);
   return hipGetLastError();
 }
 
@@ -299,9 +382,10 @@ template <int DP, bool VEC>
 static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
                             const double* bias, const double* ln2, double* part,
                             hipStream_t s) {
-  hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC>), dim3(g.p2_kblocks, g.p2_chunks),
+  const int padded = (g.p2_chunks + 7) / 8 * 8;
+  hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC>), dim3(g.p2_kblocks * padded),
                      dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
-                     g.p2_chunk, g.stat_w);
+                     g.p2_chunk, g.p2_chunks, g.p2_kblocks, g.stat_w);
   return hipGetLastError();
 }
 
