@@ -39,7 +39,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // fragment in registers up to d = 128; below or above that the vector-ALU
 // kernels run.
 static int resolve_variant(int K, int d, int variant) {
-  if (variant == kValu || variant == kMfma) return variant;
+  if (variant == kValu || variant == kMfma || variant == kX32) return variant;
   if (d <= 128 && K >= 16) return kMfma;
   return kValu;
 }
@@ -50,7 +50,7 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.K = K;
   g.d = d;
   g.variant = resolve_variant(K, d, variant);
-  if (g.variant == kMfma) {
+  if (g.variant == kMfma || g.variant == kX32) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
     g.p1_blocks = (int)((N + 127) / 128);
@@ -84,17 +84,27 @@ Geom make_geom(long N, int K, int d, int variant) {
 WsLayout make_layout(const Geom& g) {
   WsLayout L;
   size_t off = 0;
+  const bool x32 = g.variant == kX32;
   L.params = off;
-  off = align256(off + sizeof(double) * 2 * (size_t)g.Kp * g.dp);
+  off = align256(off + sizeof(double) * 2 * (size_t)g.Kp * g.dp +
+                 (x32 ? sizeof(float) * 2 * (size_t)g.Kp * g.dp : 0));
   L.bias = off;
-  off = align256(off + sizeof(double) * (size_t)g.Kp);
+  off = align256(off + sizeof(double) * (size_t)g.Kp +
+                 (x32 ? (sizeof(float) + sizeof(int)) * (size_t)g.Kp : 0));
   L.ln2 = off;
   off = align256(off + sizeof(double) * (size_t)g.N);
   L.lnsum = off;
   off = align256(off + sizeof(double) * (size_t)g.p1_blocks);
   L.part = off;
   off = align256(off + sizeof(double) * (size_t)g.p2_chunks * g.Kp * g.stat_w);
-  L.pbuf = off;
+  L.aux = off;
+  if (x32) {
+    const size_t N = (size_t)g.N;
+    off = align256(off + sizeof(float) * N);                    // m32
+    off = align256(off + sizeof(unsigned short) * 8 * N);       // slot components
+    off = align256(off + sizeof(float) * 8 * N);                // slot gammas
+    off = align256(off + N);                                    // overflow flags
+  }
   L.total = off;
   return L;
 }
@@ -146,10 +156,13 @@ static int validate_shape(long N, int K, int d, int variant) {
   if (K > 65536) return fail(FGMM_EINVAL, "K must be <= 65536 (got %d)", K);
   if (d < 1 || d > kMaxD)
     return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
-  if (variant < 0 || variant > 2)
+  if (variant < 0 || variant > 3)
     return fail(FGMM_EINVAL, "unknown variant %d", variant);
   if (variant == kMfma && d > 128)
     return fail(FGMM_EINVAL, "the MFMA variant supports d <= 128 (got %d)", d);
+  if (variant == kX32 && (d > 128 || K > 32768))
+    return fail(FGMM_EINVAL, "the x32 variant supports d <= 128 and K <= 32768 (got d=%d, K=%d)",
+                d, K);
   return FGMM_OK;
 }
 
@@ -172,13 +185,31 @@ struct Ws {
   double* ln2;
   double* lnsum;
   double* part;
+  X32Ws x;
 };
 
-static Ws carve(void* ws, const WsLayout& L) {
+static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
   char* b = static_cast<char*>(ws);
-  return Ws{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
-            reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
-            reinterpret_cast<double*>(b + L.part)};
+  Ws w{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
+       reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
+       reinterpret_cast<double*>(b + L.part), X32Ws{}};
+  if (g.variant == kX32) {
+    const size_t N = (size_t)g.N;
+    w.x.V = w.params;
+    w.x.P32 = reinterpret_cast<const float*>(w.params + 2 * (size_t)g.Kp * g.dp);
+    w.x.b64 = w.bias;
+    w.x.bias32 = reinterpret_cast<const float*>(w.bias + g.Kp);
+    w.x.exact = reinterpret_cast<const int*>(w.x.bias32 + g.Kp);
+    size_t off = L.aux;
+    w.x.m32 = reinterpret_cast<float*>(b + off);
+    off = align256(off + sizeof(float) * N);
+    w.x.ck = reinterpret_cast<unsigned short*>(b + off);
+    off = align256(off + sizeof(unsigned short) * 8 * N);
+    w.x.cg = reinterpret_cast<float*>(b + off);
+    off = align256(off + sizeof(float) * 8 * N);
+    w.x.ovf = reinterpret_cast<unsigned char*>(b + off);
+  }
+  return w;
 }
 
 static int run_precompute(const Geom& g, const float* mu, const float* var,
@@ -189,17 +220,19 @@ static int run_precompute(const Geom& g, const float* mu, const float* var,
 
 static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStream_t s) {
   Timed t(1, s);
-  hipError_t e = g.variant == kMfma
-                     ? launch_pass1_mfma(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s)
-                     : launch_pass1_valu(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s);
+  hipError_t e =
+      g.variant == kMfma  ? launch_pass1_mfma(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s)
+      : g.variant == kX32 ? launch_pass1_x32(g, X, w.x, w.ln2, ln_out, w.lnsum, s)
+                          : launch_pass1_valu(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s);
   return check_hip(e, "pass 1 (log-normalizer)");
 }
 
 static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
   Timed t(2, s);
-  hipError_t e = g.variant == kMfma
-                     ? launch_pass2_mfma(g, X, w.params, w.bias, w.ln2, w.part, s)
-                     : launch_pass2_valu(g, X, w.params, w.bias, w.ln2, w.part, s);
+  hipError_t e =
+      g.variant == kMfma  ? launch_pass2_mfma(g, X, w.params, w.bias, w.ln2, w.part, s)
+      : g.variant == kX32 ? launch_pass2_x32(g, X, w.x, w.ln2, w.part, s)
+                          : launch_pass2_valu(g, X, w.params, w.bias, w.ln2, w.part, s);
   return check_hip(e, "pass 2 (sufficient statistics)");
 }
 
@@ -237,7 +270,7 @@ int fgmm_em_fused(const float* X, const float* mu, const float* var, const float
   WsLayout L = make_layout(g);
   if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  Ws w = carve(ws, L);
+  Ws w = carve(g, ws, L);
   if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
   if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
   if ((rc = run_pass2(g, X, w, s))) return rc;
@@ -259,7 +292,7 @@ int fgmm_log_normalizer(const float* X, const float* mu, const float* var,
   WsLayout L = make_layout(g);
   if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  Ws w = carve(ws, L);
+  Ws w = carve(g, ws, L);
   if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
   return run_pass1(g, X, w, log_normalizer, s);
 }
@@ -277,7 +310,7 @@ int fgmm_accumulate_stats(const float* X, const float* mu, const float* var,
   WsLayout L = make_layout(g);
   if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  Ws w = carve(ws, L);
+  Ws w = carve(g, ws, L);
   if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
   if ((rc = check_hip(launch_ln_to_ln2(N, log_normalizer, w.ln2, s), "ln conversion")))
     return rc;
@@ -316,7 +349,7 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
   WsLayout L = make_layout(g);
   if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  Ws w = carve(ws, L);
+  Ws w = carve(g, ws, L);
   if ((rc = run_precompute(g, mu0, var0, log_pi0, w, s))) return rc;
   for (int it = 0; it < iters; it++) {
     if ((rc = run_pass1(g, X, w, nullptr, s))) return rc;

@@ -50,12 +50,15 @@ __device__ inline double block_sum_f64(double v, double* red) {
 // Writes the coefficients of component k (block-cooperative over j).
 // m / v are the fp32 parameter values of this component (nullptr for a
 // padding component, which gets zero coefficients and bias -inf).
+// The x32 variant stores the direct-form fp64 set (as VALU) plus an fp32
+// fragment-ordered expanded set behind it, and two biases.
 __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
                              const float* m, const float* v, float lp,
                              double* P, double* bias, double* red) {
   const bool real = (m != nullptr);
-  double lnv = 0.0, q = 0.0;
+  double lnv = 0.0, q = 0.0, cond = 0.0;
   const int Q = dp / 4, S1 = dp / 2;
+  float* P32 = reinterpret_cast<float*>(P + 2 * (size_t)Kp * dp);
   for (int j = threadIdx.x; j < dp; j += blockDim.x) {
     double iv = 0.0, mu = 0.0;
     if (real && j < d) {
@@ -64,10 +67,12 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
       mu = (double)m[j];
       lnv += log(vv);
       q += mu * mu * iv;
+      const double span = fabs(mu) + 4.0 * sqrt(vv);   // |x| within 4 sigma of mu
+      cond += span * span * iv;
     }
+    const int ks = k >> 4, c = k & 15, g = j / Q, t = j - g * Q;
+    const int lane = 16 * g + c;
     if (variant == kMfma) {
-      const int ks = k >> 4, c = k & 15, g = j / Q, t = j - g * Q;
-      const int lane = 16 * g + c;
       P[((size_t)ks * S1 + t) * 64 + lane] = -0.5 * kLog2e * iv;
       P[((size_t)ks * S1 + Q + t) * 64 + lane] = kLog2e * mu * iv;
     } else {
@@ -75,15 +80,35 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
       P[(size_t)k * dp + j] = sc;
       P[(size_t)Kp * dp + (size_t)k * dp + j] = mu * sc;
     }
+    if (variant == kX32) {
+      P32[((size_t)ks * S1 + t) * 64 + lane] = (float)(-0.5 * kLog2e * iv);
+      P32[((size_t)ks * S1 + Q + t) * 64 + lane] = (float)(kLog2e * mu * iv);
+    }
   }
   lnv = block_sum_f64(lnv, red);
   q = block_sum_f64(q, red);
+  if (variant == kX32) cond = block_sum_f64(cond, red);
   if (threadIdx.x == 0) {
+    float* bias32 = reinterpret_cast<float*>(bias + Kp);
+    int* exact = reinterpret_cast<int*>(bias32 + Kp);
     if (!real) {
       bias[k] = -INFINITY;
+      if (variant == kX32) {
+        bias32[k] = -INFINITY;
+        exact[k] = 0;
+      }
     } else {
       double lc = (double)lp - 0.5 * ((double)d * kLog2Pi + lnv);
       bias[k] = (variant == kMfma) ? kLog2e * (lc - 0.5 * q) : kLog2e * lc;
+      if (variant == kX32) {
+        bias32[k] = (float)(kLog2e * (lc - 0.5 * q));
+        // Rounding of the fp32 expanded distance for points near this
+        // component: ~ sqrt(2dp) * 2^-24 * log2(e) * sum_j (|mu|+4 sigma)^2/var
+        // bits.  Above 1 bit the component is evaluated exactly for every
+        // point (collapsed components, var -> 1e-6, land here).
+        const double err_bits = sqrt(2.0 * dp) * 5.9604644775390625e-8 * kLog2e * cond;
+        exact[k] = err_bits > 1.0 ? 1 : 0;
+      }
     }
   }
 }

@@ -28,7 +28,7 @@ constexpr double kLog2Pi = 1.8378770664093454835606594728112;  // ln(2*pi)
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline long round_up_l(long x, long m) { return (x + m - 1) / m * m; }
 
-enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2 };
+enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3 };
 
 // Geometry of one problem, derived once per call on the host.
 struct Geom {
@@ -36,7 +36,7 @@ struct Geom {
   int K, d;
   int dp;       // d padded to a multiple of 16
   int Kp;       // K padded to a multiple of 16
-  int variant;  // resolved (kValu or kMfma)
+  int variant;  // resolved (kValu, kMfma or kX32)
   // pass 1
   int p1_blocks;
   // pass 2
@@ -53,8 +53,25 @@ struct WsLayout {
   size_t ln2;       // fp64 [N]   base-2 log-normalizer
   size_t lnsum;     // fp64 [p1_blocks] per-workgroup sums of ln (natural)
   size_t part;      // fp64 [S][Kp][stat_w] sufficient-statistic partials
-  size_t pbuf;      // fp32 ping-pong parameter buffers for the device EM loop
+  size_t aux;       // x32 only: fp32 max ll [N], candidate slots [N][8]
+                    // (u16 component, fp32 gamma), overflow flags [N]
   size_t total;
+};
+
+// Coefficient views of the x32 variant (see fgmm_x32.hip).  The params
+// region holds the fp64 direct-form coefficients V (same layout as the VALU
+// variant) followed by the fp32 fragment-ordered coefficients; the bias
+// region holds the fp64 direct-form bias followed by the fp32 expanded bias.
+struct X32Ws {
+  const float* P32;
+  const float* bias32;
+  const int* exact;   // [Kp] 1 = evaluate this component exactly for every point
+  const double* V;
+  const double* b64;
+  float* m32;
+  unsigned short* ck;
+  float* cg;
+  unsigned char* ovf;
 };
 
 Geom make_geom(long N, int K, int d, int variant);
@@ -78,6 +95,10 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s);
+hipError_t launch_pass1_x32(const Geom& g, const float* X, const X32Ws& w, double* ln2,
+                            float* ln_out, double* lnsum, hipStream_t s);
+hipError_t launch_pass2_x32(const Geom& g, const float* X, const X32Ws& w,
+                            const double* ln2, double* part, hipStream_t s);
 // Caller-supplied fp32 natural-log normalizer -> internal fp64 base-2 copy.
 hipError_t launch_ln_to_ln2(long N, const float* ln, double* ln2, hipStream_t s);
 // Standalone M-step on caller-provided fp32 statistics.

@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
       }
       pre[i] = v;
     }
-    if (tid < kP2Tile) preL = (t0 + tid < p1) ? ln2[t0 + tid] : 0.0;
+    if (tid < kP2Tile) preL = (t0 + tid < p1) ? ln2[t0 + tid] : INFINITY;  // gamma = 0 past the chunk
   };
   auto lstore = [&](int buf) {
 #pragma unroll
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
         for (int r = 0; r < 4; r++) {
           const int pl = sub * 16 + 4 * r + g;
           const double ll = a0[r] + a1[r];
-          gm[r] = (t0 + pl < p1) ? exp2f((float)(ll - ls[buf][pl])) : 0.f;
+          gm[r] = exp2f((float)(ll - ls[buf][pl]));
           nk += (double)gm[r];
         }
         const float* xsub = xt + sub * 16 * XS;

@@ -22,8 +22,10 @@
  * least fgmm_workspace_bytes(N, K, d, variant) bytes, 256-byte aligned.  The
  * library allocates no device memory of its own on these paths.
  *
- * variant: FGMM_VARIANT_AUTO picks matrix-core or vector-ALU kernels from a
- * table keyed by (K, d); FGMM_VARIANT_VALU / FGMM_VARIANT_MFMA force one.
+ * variant: FGMM_VARIANT_AUTO picks a kernel family from a table keyed by
+ * (K, d); FGMM_VARIANT_VALU (fp64 vector ALU), FGMM_VARIANT_MFMA (fp64
+ * matrix-core distance) or FGMM_VARIANT_X32 (fp32 matrix-core distance with
+ * the significant pairs recomputed in fp64) force one.
  */
 #ifndef FLASHGMM_H
 #define FLASHGMM_H
@@ -42,6 +44,7 @@ extern "C" {
 #define FGMM_VARIANT_AUTO 0
 #define FGMM_VARIANT_VALU 1
 #define FGMM_VARIANT_MFMA 2
+#define FGMM_VARIANT_X32 3   /* fp32 matrix-core distance + exact fp64 refinement */
 
 /* Library ABI version (major*100 + minor). */
 int fgmm_version(void);

@@ -69,7 +69,7 @@ def to_dev(cuda, *arrs):
 def variants_for(K, d):
     v = ["valu"]
     if d <= 128:
-        v.append("mfma")
+        v += ["mfma", "x32"]
     return v
 
 
@@ -119,7 +119,7 @@ def test_golden_vectors(cuda, name):
     with np.load(path, allow_pickle=False) as z:
         g = {k: z[k] for k in z.files}
     t = to_dev(cuda, g["X"], g["mu"], g["var"], g["log_pi"])
-    for variant in ("valu", "mfma"):
+    for variant in ("valu", "mfma", "x32"):
         print(f"[case] golden {name} variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], g["ln"], f"{name} {variant}")
@@ -270,7 +270,7 @@ def test_unaligned_and_noncontiguous_inputs(cuda):
     Xu = big[1:].view(X.shape)                    # 4-byte offset: scalar load path
     assert Xu.data_ptr() % 16 != 0
     t = to_dev(cuda, mu, var, lp)
-    for variant in ("valu", "mfma"):
+    for variant in ("valu", "mfma", "x32"):
         print(f"[case] unaligned X variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(Xu, *t, variant=variant)]
         check_params(out[:3], ref[:3], f"unaligned {variant}")
