@@ -31,6 +31,11 @@ SIGNATURES = {
     "fgmm_accumulate_stats": ([_P, _P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _P, _Z, _P], _I),
     "fgmm_m_step_update": ([_P, _P, _P, _L, _I, _I, _P, _P, _P, _P], _I),
     "fgmm_em_fit": ([_P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _P, _P, _P, _P, _Z, _P], _I),
+    "fgmm_flash_e_step": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _Z, _P], _I),
+    "fgmm_standard_e_step_workspace_bytes": ([_L, _I, _I, _I], _Z),
+    "fgmm_standard_e_step": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _Z, _P], _I),
+    "fgmm_standard_m_step_workspace_bytes": ([_L, _I, _I], _Z),
+    "fgmm_standard_m_step": ([_P, _P, _L, _I, _I, _P, _P, _P, _P, _Z, _P], _I),
     "fgmm_profile_enable": ([_I], _I),
     "fgmm_profile_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)], _I),
 }

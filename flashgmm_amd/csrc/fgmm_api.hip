@@ -236,6 +236,33 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
   return check_hip(e, "pass 2 (sufficient statistics)");
 }
 
+// The gamma-returning E-steps have no x32 form: the candidate scheme pays off
+// only when gamma is consumed on chip, so they run the fp64 matrix-core path.
+static int estep_variant(int variant) { return variant == kX32 ? kMfma : variant; }
+
+// Standard E-step workspace: the common regions, then the fp64 matrix L.
+static size_t lmat_offset(const WsLayout& L) { return L.total; }
+static size_t std_estep_bytes(const Geom& g, const WsLayout& L) {
+  return align256(lmat_offset(L) + sizeof(double) * (size_t)g.N * g.K);
+}
+
+// Standard M-step geometry: the MFMA chunking (its kernel needs no
+// coefficient registers, so every d <= 256 runs on the matrix cores) and a
+// workspace of the stats partials only.
+static Geom mstep_geom(long N, int K, int d) { return make_geom(N, K, d, kMfma); }
+static size_t mstep_bytes(const Geom& g) {
+  return align256(sizeof(double) * (size_t)g.p2_chunks * g.Kp * g.stat_w);
+}
+
+static int validate_ws_bytes(void* ws, size_t bytes, size_t need) {
+  if (ws == nullptr) return fail(FGMM_EWORKSPACE, "workspace pointer is NULL");
+  if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0)
+    return fail(FGMM_EWORKSPACE, "workspace must be 256-byte aligned");
+  if (bytes < need)
+    return fail(FGMM_EWORKSPACE, "workspace too small: %zu bytes given, %zu needed", bytes, need);
+  return FGMM_OK;
+}
+
 }  // namespace fgmm
 
 using namespace fgmm;
@@ -363,6 +390,88 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
     if (rc) return rc;
   }
   return FGMM_OK;
+}
+
+int fgmm_flash_e_step(const float* X, const float* mu, const float* var, const float* log_pi,
+                      long N, int K, int d, int variant, float* gamma, float* log_normalizer,
+                      void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  variant = estep_variant(variant);
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  FGMM_REQUIRE(gamma); FGMM_REQUIRE(log_normalizer);
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(g, ws, L);
+  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
+  if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
+  Timed t(2, s);
+  return check_hip(launch_sweep(g, kSweepGamma, X, w.params, w.bias, w.ln2, gamma, nullptr, s),
+                   "gamma sweep");
+}
+
+size_t fgmm_standard_e_step_workspace_bytes(long N, int K, int d, int variant) {
+  variant = estep_variant(variant);
+  if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
+  Geom g = make_geom(N, K, d, variant);
+  return std_estep_bytes(g, make_layout(g));
+}
+
+int fgmm_standard_e_step(const float* X, const float* mu, const float* var,
+                         const float* log_pi, long N, int K, int d, int variant, float* gamma,
+                         float* log_normalizer, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  variant = estep_variant(variant);
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  FGMM_REQUIRE(gamma); FGMM_REQUIRE(log_normalizer);
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  if ((rc = validate_ws_bytes(ws, ws_bytes, std_estep_bytes(g, L)))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(g, ws, L);
+  double* Lmat = reinterpret_cast<double*>(static_cast<char*>(ws) + lmat_offset(L));
+  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
+  {
+    Timed t(1, s);
+    rc = check_hip(launch_sweep(g, kSweepLL, X, w.params, w.bias, nullptr, nullptr, Lmat, s),
+                   "log-likelihood matrix");
+    if (rc) return rc;
+  }
+  Timed t(2, s);
+  return check_hip(launch_lse_rows(N, K, Lmat, gamma, log_normalizer, s), "row log-sum-exp");
+}
+
+size_t fgmm_standard_m_step_workspace_bytes(long N, int K, int d) {
+  if (validate_shape(N, K, d, kAuto) != FGMM_OK) return 0;
+  return mstep_bytes(mstep_geom(N, K, d));
+}
+
+int fgmm_standard_m_step(const float* X, const float* gamma, long N, int K, int d,
+                         float* mu, float* var, float* log_pi, void* ws, size_t ws_bytes,
+                         void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, kAuto);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(gamma);
+  FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  Geom g = mstep_geom(N, K, d);
+  if ((rc = validate_ws_bytes(ws, ws_bytes, mstep_bytes(g)))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  double* part = static_cast<double*>(ws);
+  {
+    Timed t(2, s);
+    if ((rc = check_hip(launch_gamma_stats(g, X, gamma, part, s), "statistics from gamma")))
+      return rc;
+  }
+  Timed t(3, s);
+  return check_hip(launch_reduce(g, part, nullptr, nullptr, nullptr, nullptr, mu, var, log_pi,
+                                 nullptr, nullptr, nullptr, s, /*standard=*/1),
+                   "standard M-step");
 }
 
 int fgmm_profile_enable(int enable) {

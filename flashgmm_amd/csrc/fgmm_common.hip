@@ -149,7 +149,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               float* __restrict__ new_var,
                               float* __restrict__ new_log_pi,
                               double* __restrict__ P_next, double* __restrict__ bias_next,
-                              double* __restrict__ ll_out) {
+                              double* __restrict__ ll_out, int standard) {
   __shared__ double red[16];
   __shared__ double nk_sh;
   __shared__ float mu_sh[kMaxD], var_sh[kMaxD];
@@ -180,7 +180,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   }
   __syncthreads();
   const double nk = nk_sh;
-  const double inv = 1.0 / (nk > 1e-8 ? nk : 1e-8);
+  const double inv = standard ? 1.0 / nk : 1.0 / (nk > 1e-8 ? nk : 1e-8);
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
     double a = 0.0, b = 0.0;
     const double* p = part + (size_t)k * row;
@@ -196,7 +196,9 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     if (new_mu != nullptr) {
       double m = a * inv;
       double v = b * inv - m * m;
-      v = v > 1e-6 ? v : 1e-6;
+      // flash: fmaxf-style floor; standard: clamp_min, which keeps the NaN of
+      // an empty component
+      v = standard ? (v < 1e-6 ? 1e-6 : v) : (v > 1e-6 ? v : 1e-6);
       float mf = (float)m, vf = (float)v;
       new_mu[(size_t)k * d + j] = mf;
       new_var[(size_t)k * d + j] = vf;
@@ -207,7 +209,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   float lpf = 0.f;
   if (new_log_pi != nullptr) {
     double p = nk / (double)N;
-    lpf = (float)log(p > 1e-8 ? p : 1e-8);
+    lpf = (float)log(standard ? p : (p > 1e-8 ? p : 1e-8));
     if (threadIdx.x == 0) new_log_pi[k] = lpf;
   }
   if (n_k != nullptr && threadIdx.x == 0) n_k[k] = (float)nk;
@@ -220,12 +222,12 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
 hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
-                         double* bias_next, double* ll_out, hipStream_t s) {
+                         double* bias_next, double* ll_out, hipStream_t s, int standard) {
   const int blocks = params_next != nullptr ? g.Kp : g.K;
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
-                     bias_next, ll_out);
+                     bias_next, ll_out, standard);
   return hipGetLastError();
 }
 

@@ -30,6 +30,11 @@ inline long round_up_l(long x, long m) { return (x + m - 1) / m * m; }
 
 enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3 };
 
+// What a sweep of the Pass-1 kernels over all components produces per point:
+// the log-normalizer (online log-sum-exp), gamma[n][k] from a known
+// log-normalizer, or the fp64 log-likelihood matrix row L[n][k].
+enum Sweep : int { kSweepLse = 0, kSweepGamma = 1, kSweepLL = 2 };
+
 // Geometry of one problem, derived once per call on the host.
 struct Geom {
   long N;
@@ -91,10 +96,27 @@ hipError_t launch_pass2(const Geom& g, const float* X, const double* params,
 // (n_k, s_k, sq_k), fp32 new parameters (M-step with the native clamps),
 // the precomputed coefficients for the next iteration (params_next/bias_next),
 // and ll_out = sum(lnsum)/N.
+// standard != 0 selects the standard M-step's arithmetic (no clamp on n_k or
+// n_k/N); the variance floor 1e-6 applies to both.
 hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
-                         double* bias_next, double* ll_out, hipStream_t s);
+                         double* bias_next, double* ll_out, hipStream_t s,
+                         int standard = 0);
+// Pass-1 sweep in one of the Sweep modes (the MFMA or VALU kernels by
+// g.variant).  kSweepGamma reads ln2 and writes gamma [N][K] (fp32);
+// kSweepLL writes Lmat [N][K] (fp64, base 2).
+hipError_t launch_sweep(const Geom& g, int sweep, const float* X, const double* params,
+                        const double* bias, double* ln2, float* gamma, double* Lmat,
+                        hipStream_t s);
+// Row-wise log-sum-exp of Lmat [N][K] (base 2) -> log_normalizer (natural,
+// fp32) and gamma = 2^(L - lse) (fp32).
+hipError_t launch_lse_rows(long N, int K, const double* Lmat, float* gamma,
+                           float* log_normalizer, hipStream_t s);
+// Sufficient statistics from a caller-supplied gamma [N][K] (fp32) into the
+// Pass-2 partial layout of g (g describes an MFMA geometry; d <= 256).
+hipError_t launch_gamma_stats(const Geom& g, const float* X, const float* gamma,
+                              double* part, hipStream_t s);
 hipError_t launch_pass1_x32(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                             float* ln_out, double* lnsum, hipStream_t s);
 hipError_t launch_pass2_x32(const Geom& g, const float* X, const X32Ws& w,

@@ -75,11 +75,17 @@ __device__ inline void load_quarter(const float* __restrict__ X, long n, long N,
 // an online (max, sum) over the 4 components per subtile its accumulator
 // rows hold; the four lane groups merge at the end.
 // ---------------------------------------------------------------------------
-template <int DP, bool VEC>
+//
+// The same sweep also materialises per-pair values for the gamma-returning
+// E-steps: SWEEP == kSweepGamma writes gamma[n][k] = 2^(ll2 - ln2[n]) (ln2 read
+// from a previous log-normalizer sweep), SWEEP == kSweepLL writes the fp64
+// matrix L[n][k] = ll2 the standard E-step normalises row by row.
+template <int DP, bool VEC, int SWEEP>
 __global__ __launch_bounds__(512) void pass1_mfma_kernel(
-    const float* __restrict__ X, long N, int d, int Kp, const double* __restrict__ P,
+    const float* __restrict__ X, long N, int d, int K, int Kp, const double* __restrict__ P,
     const double* __restrict__ bias, double* __restrict__ ln2,
-    float* __restrict__ ln_out, double* __restrict__ lnsum) {
+    float* __restrict__ ln_out, double* __restrict__ lnsum, float* __restrict__ gamma,
+    double* __restrict__ Lmat) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int TILE = kP1Sub * S1 * 64;        // doubles per K tile
   constexpr int PER = TILE / 2 / kP1Threads;    // double2 per thread per tile
@@ -93,6 +99,9 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
 
   float xq[Q];
   load_quarter<Q, VEC>(X, n, N, d, g * Q, xq);
+  const bool live = n < N;
+  double l2n = 0.0;
+  if constexpr (SWEEP == kSweepGamma) l2n = live ? ln2[n] : 0.0;
 
   const int ntiles = Kp / (16 * kP1Sub);
   // staging registers for the next coefficient tile (clang vector type so
@@ -135,21 +144,38 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
       acc0 = mfma64(sP[(0 * S1 + s) * 64 + lane], b, acc0);
       acc1 = mfma64(sP[(1 * S1 + s) * 64 + lane], b, acc1);
     }
-    double vmax = acc0[0];
+    if constexpr (SWEEP == kSweepLse) {
+      double vmax = acc0[0];
 #pragma unroll
-    for (int r = 0; r < 4; r++) vmax = fmax(vmax, fmax(acc0[r], acc1[r]));
-    const double mn = fmax(m, vmax);
-    double add = 0.0;
+      for (int r = 0; r < 4; r++) vmax = fmax(vmax, fmax(acc0[r], acc1[r]));
+      const double mn = fmax(m, vmax);
+      double add = 0.0;
 #pragma unroll
-    for (int r = 0; r < 4; r++)
-      add += (double)exp2f((float)(acc0[r] - mn)) + (double)exp2f((float)(acc1[r] - mn));
-    ssum = ssum * (double)exp2f((float)(m - mn)) + add;
-    m = mn;
+      for (int r = 0; r < 4; r++)
+        add += (double)exp2f((float)(acc0[r] - mn)) + (double)exp2f((float)(acc1[r] - mn));
+      ssum = ssum * (double)exp2f((float)(m - mn)) + add;
+      m = mn;
+    } else if (live) {
+      // register r of lane (g, c) holds component 4r+g of the subtile for point c
+      const int kt = t * 16 * kP1Sub;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int k0 = kt + 4 * r + g, k1 = k0 + 16;
+        if constexpr (SWEEP == kSweepGamma) {
+          if (k0 < K) gamma[(size_t)n * K + k0] = exp2f((float)(acc0[r] - l2n));
+          if (k1 < K) gamma[(size_t)n * K + k1] = exp2f((float)(acc1[r] - l2n));
+        } else {
+          if (k0 < K) Lmat[(size_t)n * K + k0] = acc0[r];
+          if (k1 < K) Lmat[(size_t)n * K + k1] = acc1[r];
+        }
+      }
+    }
     if (t + 1 < ntiles) FGMM_P1_LSTORE(buf ^ 1)
     __syncthreads();
   }
 #undef FGMM_P1_GLOAD
 #undef FGMM_P1_LSTORE
+  if constexpr (SWEEP != kSweepLse) return;
   // merge the four lane groups holding the same point
 #pragma unroll
   for (int off = 16; off <= 32; off <<= 1) {
@@ -161,7 +187,7 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
   }
   const double l2 = m + log2(ssum);
   const double lnat = l2 * kLn2;
-  const bool own = (g == 0) && (n < N);
+  const bool own = (g == 0) && live;
   if (own) {
     ln2[n] = l2;
     if (ln_out != nullptr) ln_out[n] = (float)lnat;
@@ -361,21 +387,37 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-template <int DP, bool VEC>
+template <int DP, bool VEC, int SWEEP>
 static hipError_t p1_launch(const Geom& g, const float* X, const double* P,
                             const double* bias, double* ln2, float* ln_out,
-                            double* lnsum, hipStream_t s) {
+                            double* lnsum, float* gamma, double* Lmat, hipStream_t s) {
   constexpr size_t lds = 2 * (size_t)kP1Sub * (DP / 2) * 64 * sizeof(double);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)pass1_mfma_kernel<DP, VEC>,
+    hipError_t e = hipFuncSetAttribute((const void*)pass1_mfma_kernel<DP, VEC, SWEEP>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((pass1_mfma_kernel<DP, VEC>), dim3(g.p1_blocks), dim3(kP1Threads), lds, s,
-                     X, g.N, g.d, g.Kp, P, bias, ln2, ln_out, lnsum);
+  hipLaunchKernelGGL((pass1_mfma_kernel<DP, VEC, SWEEP>), dim3(g.p1_blocks), dim3(kP1Threads),
+                     lds, s, X, g.N, g.d, g.K, g.Kp, P, bias, ln2, ln_out, lnsum, gamma, Lmat);
   return hipGetLastError();
+}
+
+template <int DP>
+static hipError_t p1_sweep(const Geom& g, bool v, int sweep, const float* X, const double* P,
+                           const double* bias, double* ln2, float* ln_out, double* lnsum,
+                           float* gamma, double* Lmat, hipStream_t s) {
+#define FGMM_P1S(SW)                                                                   \
+  return v ? p1_launch<DP, true, SW>(g, X, P, bias, ln2, ln_out, lnsum, gamma, Lmat, s) \
+           : p1_launch<DP, false, SW>(g, X, P, bias, ln2, ln_out, lnsum, gamma, Lmat, s);
+  switch (sweep) {
+    case kSweepLse: FGMM_P1S(kSweepLse)
+    case kSweepGamma: FGMM_P1S(kSweepGamma)
+    case kSweepLL: FGMM_P1S(kSweepLL)
+    default: return hipErrorInvalidValue;
+  }
+#undef FGMM_P1S
 }
 
 template <int DP, bool VEC>
@@ -393,21 +435,26 @@ bool x_is_vec(const float* X, int d) {
   return (d % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0);
 }
 
-hipError_t launch_pass1_mfma(const Geom& g, const float* X, const double* P,
-                             const double* bias, double* ln2, float* ln_out,
-                             double* lnsum, hipStream_t s) {
+hipError_t launch_sweep_mfma(const Geom& g, int sweep, const float* X, const double* P,
+                             const double* bias, double* ln2, float* ln_out, double* lnsum,
+                             float* gamma, double* Lmat, hipStream_t s) {
   const bool v = x_is_vec(X, g.d);
   switch (g.dp) {
-#define FGMM_P1(D)                                                              \
-  case D:                                                                      \
-    return v ? p1_launch<D, true>(g, X, P, bias, ln2, ln_out, lnsum, s)         \
-             : p1_launch<D, false>(g, X, P, bias, ln2, ln_out, lnsum, s);
+#define FGMM_P1(D)                                                                      \
+  case D:                                                                              \
+    return p1_sweep<D>(g, v, sweep, X, P, bias, ln2, ln_out, lnsum, gamma, Lmat, s);
     FGMM_P1(16) FGMM_P1(32) FGMM_P1(48) FGMM_P1(64) FGMM_P1(80) FGMM_P1(96)
     FGMM_P1(112) FGMM_P1(128)
 #undef FGMM_P1
     default:
       return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_pass1_mfma(const Geom& g, const float* X, const double* P,
+                             const double* bias, double* ln2, float* ln_out,
+                             double* lnsum, hipStream_t s) {
+  return launch_sweep_mfma(g, kSweepLse, X, P, bias, ln2, ln_out, lnsum, nullptr, nullptr, s);
 }
 
 hipError_t launch_pass2_mfma(const Geom& g, const float* X, const double* P,

@@ -24,11 +24,14 @@ constexpr int kV2Tile = 64;     // Pass 2: points per LDS tile
 // (column j of all points contiguous) so each (j) read is one conflict-free
 // LDS access; components are processed four at a time to reuse it.
 // ---------------------------------------------------------------------------
-template <int DP>
+// SWEEP selects the output (see Sweep): the log-normalizer, gamma[n][k]
+// from a known log-normalizer, or the fp64 matrix L[n][k].
+template <int DP, int SWEEP>
 __global__ __launch_bounds__(64) void pass1_valu_kernel(
     const float* __restrict__ X, long N, int d, int K, int Kp,
     const double* __restrict__ P, const double* __restrict__ bias,
-    double* __restrict__ ln2, float* __restrict__ ln_out, double* __restrict__ lnsum) {
+    double* __restrict__ ln2, float* __restrict__ ln_out, double* __restrict__ lnsum,
+    float* __restrict__ gamma, double* __restrict__ Lmat) {
   constexpr int XS = kV1Points + 1;
   __shared__ float xs[DP * XS];
   const int lane = threadIdx.x;
@@ -40,6 +43,9 @@ __global__ __launch_bounds__(64) void pass1_valu_kernel(
   }
   __syncthreads();
   const long n = base + lane;
+  const bool live = n < N;
+  double l2n = 0.0;
+  if constexpr (SWEEP == kSweepGamma) l2n = live ? ln2[n] : 0.0;
   const double* S = P;
   const double* MS = P + (size_t)Kp * DP;
   double m = -DBL_MAX, ssum = 0.0;
@@ -60,15 +66,22 @@ __global__ __launch_bounds__(64) void pass1_valu_kernel(
     for (int u = 0; u < 4; u++) {
       if (k0 + u < K) {
         const double v = bias[kk[u]] - acc[u];
-        const double mn = fmax(m, v);
-        ssum = ssum * (double)exp2f((float)(m - mn)) + (double)exp2f((float)(v - mn));
-        m = mn;
+        if constexpr (SWEEP == kSweepLse) {
+          const double mn = fmax(m, v);
+          ssum = ssum * (double)exp2f((float)(m - mn)) + (double)exp2f((float)(v - mn));
+          m = mn;
+        } else if constexpr (SWEEP == kSweepGamma) {
+          if (live) gamma[(size_t)n * K + k0 + u] = exp2f((float)(v - l2n));
+        } else {
+          if (live) Lmat[(size_t)n * K + k0 + u] = v;
+        }
       }
     }
   }
+  if constexpr (SWEEP != kSweepLse) return;
   const double l2 = m + log2(ssum);
   const double lnat = l2 * kLn2;
-  const bool own = n < N;
+  const bool own = live;
   if (own) {
     ln2[n] = l2;
     if (ln_out != nullptr) ln_out[n] = (float)lnat;
@@ -176,11 +189,20 @@ __global__ __launch_bounds__(256) void pass2_valu_kernel(
 }
 
 template <int DP>
-static hipError_t v1_launch(const Geom& g, const float* X, const double* P,
+static hipError_t v1_launch(const Geom& g, int sweep, const float* X, const double* P,
                             const double* bias, double* ln2, float* ln_out,
-                            double* lnsum, hipStream_t s) {
-  hipLaunchKernelGGL((pass1_valu_kernel<DP>), dim3(g.p1_blocks), dim3(64), 0, s, X, g.N,
-                     g.d, g.K, g.Kp, P, bias, ln2, ln_out, lnsum);
+                            double* lnsum, float* gamma, double* Lmat, hipStream_t s) {
+  switch (sweep) {
+#define FGMM_V1S(SW)                                                                    \
+  case SW:                                                                             \
+    hipLaunchKernelGGL((pass1_valu_kernel<DP, SW>), dim3(g.p1_blocks), dim3(64), 0, s, X, \
+                       g.N, g.d, g.K, g.Kp, P, bias, ln2, ln_out, lnsum, gamma, Lmat);  \
+    break;
+    FGMM_V1S(kSweepLse) FGMM_V1S(kSweepGamma) FGMM_V1S(kSweepLL)
+#undef FGMM_V1S
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -193,17 +215,22 @@ static hipError_t v2_launch(const Geom& g, const float* X, const double* P,
   return hipGetLastError();
 }
 
+hipError_t launch_sweep_valu(const Geom& g, int sweep, const float* X, const double* P,
+                             const double* bias, double* ln2, float* ln_out, double* lnsum,
+                             float* gamma, double* Lmat, hipStream_t s) {
+  switch (g.dp) {
+#define FGMM_V1(D) \
+  case D: return v1_launch<D>(g, sweep, X, P, bias, ln2, ln_out, lnsum, gamma, Lmat, s);
+    FGMM_V1(16) FGMM_V1(32) FGMM_V1(64) FGMM_V1(128) FGMM_V1(256)
+#undef FGMM_V1
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_pass1_valu(const Geom& g, const float* X, const double* P,
                              const double* bias, double* ln2, float* ln_out,
                              double* lnsum, hipStream_t s) {
-  switch (g.dp) {
-    case 16: return v1_launch<16>(g, X, P, bias, ln2, ln_out, lnsum, s);
-    case 32: return v1_launch<32>(g, X, P, bias, ln2, ln_out, lnsum, s);
-    case 64: return v1_launch<64>(g, X, P, bias, ln2, ln_out, lnsum, s);
-    case 128: return v1_launch<128>(g, X, P, bias, ln2, ln_out, lnsum, s);
-    case 256: return v1_launch<256>(g, X, P, bias, ln2, ln_out, lnsum, s);
-    default: return hipErrorInvalidValue;
-  }
+  return launch_sweep_valu(g, kSweepLse, X, P, bias, ln2, ln_out, lnsum, nullptr, nullptr, s);
 }
 
 hipError_t launch_pass2_valu(const Geom& g, const float* X, const double* P,

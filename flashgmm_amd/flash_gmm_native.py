@@ -1,9 +1,11 @@
 """Drop-in for the reference's ``flash_gmm_native`` extension module on ROCm.
 
 Same function names, argument order, defaults and return order as the
-reference's pybind11 module (``flash_gmm/csrc/binding.cpp:94-109``), plus the
-three stage entry points (``flash_log_normalizer``, ``flash_accumulate_stats``,
-``m_step_update``).  Every call goes to ``libflashgmm.so`` (hand-written HIP
+reference's pybind11 module (``flash_gmm/csrc/binding.cpp:94-109``:
+``standard_e_step``, ``flash_e_step``, ``flash_em_fused``, ``standard_m_step``),
+plus the three stage entry points (``flash_log_normalizer``,
+``flash_accumulate_stats``, ``m_step_update``) and the device-resident loop
+``em_fit``.  Every call goes to ``libflashgmm.so`` (hand-written HIP
 kernels for gfx950) on torch's current stream; tensors must live on a ROCm
 device.  Outputs are fresh tensors; inputs are never modified.
 
@@ -14,7 +16,9 @@ check keeps the reference's message ("X must be float32",
 
 The reference dispatches CPU tensors to its OpenMP path
 (``binding.cpp:48,59,75,91``).  This module accelerates the ROCm path only and
-raises on CPU tensors instead of computing elsewhere.
+raises on CPU tensors instead of computing elsewhere.  Conversely the
+reference refuses ``flash_e_step`` on CUDA tensors (``binding.cpp:55-57``);
+here it runs on the device.
 """
 from __future__ import annotations
 
@@ -130,6 +134,86 @@ def flash_accumulate_stats(X, mu, var, log_pi, log_normalizer, *, variant=None):
                                          N, K, d, v, _ptr(n_k), _ptr(s_k), _ptr(sq_k),
                                          _ptr(ws), nbytes, _lib.stream_handle(X.device)))
     return [n_k, s_k, sq_k]
+
+
+def _gamma_estep(X, mu, var, log_pi, variant, fn, standard):
+    X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, fn)
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    gamma = torch.empty((N, K), dtype=torch.float32, device=X.device)
+    ln = torch.empty((N,), dtype=torch.float32, device=X.device)
+    stream = _lib.stream_handle(X.device)
+    if standard:
+        # the N x K fp64 matrix lives only for this call, like the reference's L
+        nbytes = lib.fgmm_standard_e_step_workspace_bytes(N, K, d, v)
+        if nbytes == 0:
+            raise RuntimeError("flashgmm_amd: " + lib.fgmm_last_error().decode(errors="replace"))
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=X.device)
+        _lib.check(lib.fgmm_standard_e_step(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K,
+                                            d, v, _ptr(gamma), _ptr(ln), _ptr(ws), nbytes,
+                                            stream))
+    else:
+        ws, nbytes = _ws(X, N, K, d, v)
+        _lib.check(lib.fgmm_flash_e_step(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d,
+                                         v, _ptr(gamma), _ptr(ln), _ptr(ws), nbytes, stream))
+    return [gamma, ln]
+
+
+def standard_e_step(X, mu, var, log_pi, *, variant=None):
+    """Materialising E-step; returns ``[gamma, log_normalizer]``
+    (``binding.cpp:35-49``, ``flash_gmm_cuda.cu:328-400``).  The N x K
+    log-density matrix is formed in fp64 on the device and normalised row by
+    row."""
+    return _gamma_estep(X, mu, var, log_pi, variant, "standard_e_step", standard=True)
+
+
+def flash_e_step(X, mu, var, log_pi, BK: int = 4, *, variant=None):
+    """Flash E-step returning gamma; returns ``[gamma, log_normalizer]``
+    (``binding.cpp:51-60``; CPU-only in the reference,
+    ``flash_gmm_cpu.cpp:108-168``).  Pass 1 gives the log-normalizer, a second
+    sweep writes gamma.  ``BK`` is accepted for signature compatibility."""
+    if int(BK) < 1:
+        raise RuntimeError(f"flashgmm_amd.flash_e_step: BK must be >= 1 (got {BK})")
+    return _gamma_estep(X, mu, var, log_pi, variant, "flash_e_step", standard=False)
+
+
+def standard_m_step(X, gamma):
+    """M-step from responsibilities; returns ``[mu, var, log_pi]`` with the
+    reference's standard arithmetic: no clamp on ``n_k``, ``var`` floored at
+    1e-6, ``log_pi = log(n_k / N)`` (``binding.cpp:78-92``,
+    ``flash_gmm_cpu.cpp:292-311``)."""
+    if X.dtype != torch.float32:
+        raise RuntimeError("X must be float32")
+    if X.dim() != 2:
+        raise RuntimeError("X must be 2D")
+    _check_device(X, "standard_m_step")
+    N, d = X.shape
+    if N < 1 or d < 1:
+        raise RuntimeError(f"flashgmm_amd.standard_m_step: X must be non-empty "
+                           f"(got {tuple(X.shape)})")
+    if gamma.dim() != 2 or gamma.shape[0] != N or gamma.shape[1] < 1:
+        raise RuntimeError(f"flashgmm_amd.standard_m_step: gamma must be [{N}, K] "
+                           f"(got {tuple(gamma.shape)})")
+    if gamma.dtype != torch.float32:
+        raise RuntimeError(f"flashgmm_amd.standard_m_step: gamma must be float32 "
+                           f"(got {gamma.dtype})")
+    if gamma.device != X.device:
+        raise RuntimeError(f"flashgmm_amd.standard_m_step: gamma is on {gamma.device}, "
+                           f"X on {X.device}")
+    K = gamma.shape[1]
+    X, gamma = X.contiguous(), gamma.contiguous()
+    lib = _lib.load()
+    nbytes = lib.fgmm_standard_m_step_workspace_bytes(N, K, d)
+    if nbytes == 0:
+        raise RuntimeError("flashgmm_amd: " + lib.fgmm_last_error().decode(errors="replace"))
+    ws = _lib.workspace(X.device, nbytes)
+    mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    var = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
+    _lib.check(lib.fgmm_standard_m_step(_ptr(X), _ptr(gamma), N, K, d, _ptr(mu), _ptr(var),
+                                        _ptr(log_pi), _ptr(ws), nbytes,
+                                        _lib.stream_handle(X.device)))
+    return [mu, var, log_pi]
 
 
 def m_step_update(n_k, s_k, sq_k, N: int):

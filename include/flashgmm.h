@@ -19,8 +19,9 @@
  * Argument errors are detected before any device work is queued.
  *
  * Workspace: entry points that take (ws, ws_bytes) need a device buffer of at
- * least fgmm_workspace_bytes(N, K, d, variant) bytes, 256-byte aligned.  The
- * library allocates no device memory of its own on these paths.
+ * least fgmm_workspace_bytes(N, K, d, variant) bytes, 256-byte aligned
+ * (fgmm_standard_e_step and fgmm_standard_m_step: their own *_workspace_bytes
+ * query).  The library allocates no device memory of its own on these paths.
  *
  * variant: FGMM_VARIANT_AUTO picks a kernel family from a table keyed by
  * (K, d); FGMM_VARIANT_VALU (fp64 vector ALU), FGMM_VARIANT_MFMA (fp64
@@ -119,6 +120,52 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0,
                 const float* log_pi0, long N, int K, int d, int iters, int variant,
                 float* mu_out, float* var_out, float* log_pi_out, double* ll_traj,
                 void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Gamma-returning E-step on the flash schedule: Pass 1 (log-normalizer), then
+ * a second sweep that recomputes every (n, k) log-density and writes
+ * gamma[N][K] = exp(ll - log_normalizer).  No other N x K array is formed.
+ * Workspace: fgmm_workspace_bytes.  FGMM_VARIANT_X32 runs as MFMA here.
+ * Replaces flash_e_step (flash_gmm/csrc/binding.cpp:51-60,97-99), which the
+ * reference implements on the CPU only (flash_gmm_cpu.cpp:108-168) and
+ * refuses for CUDA tensors.
+ */
+int fgmm_flash_e_step(const float* X, const float* mu, const float* var,
+                      const float* log_pi, long N, int K, int d, int variant,
+                      float* gamma, float* log_normalizer, void* ws, size_t ws_bytes,
+                      void* stream);
+
+/* Workspace bytes of fgmm_standard_e_step (includes the N x K fp64 matrix). */
+size_t fgmm_standard_e_step_workspace_bytes(long N, int K, int d, int variant);
+
+/*
+ * Standard (materialising) E-step: the log-density matrix L[N][K] is written
+ * to the workspace in fp64, then a row log-sum-exp writes
+ * log_normalizer[N] and gamma[N][K] = exp(L - log_normalizer).
+ * FGMM_VARIANT_X32 runs as MFMA here.
+ * Replaces standard_e_step_cuda = standard_e_step_kernel +
+ * logsumexp_normalize_kernel (flash_gmm/csrc/flash_gmm_cuda.cu:328-400),
+ * bound as standard_e_step (flash_gmm/csrc/binding.cpp:35-49,95-96).
+ */
+int fgmm_standard_e_step(const float* X, const float* mu, const float* var,
+                         const float* log_pi, long N, int K, int d, int variant,
+                         float* gamma, float* log_normalizer, void* ws, size_t ws_bytes,
+                         void* stream);
+
+/* Workspace bytes of fgmm_standard_m_step. */
+size_t fgmm_standard_m_step_workspace_bytes(long N, int K, int d);
+
+/*
+ * Standard M-step from a given gamma[N][K] (fp32, device):
+ * n_k = sum_n gamma, mu = gamma^T X / n_k, var = max(gamma^T X^2 / n_k - mu^2,
+ * 1e-6), log_pi = log(n_k / N) -- no clamp on n_k (a component with
+ * n_k = 0 gets NaN mu and -inf log_pi, as in the reference).
+ * Replaces standard_m_step (flash_gmm/csrc/binding.cpp:78-92, ATen GEMMs on
+ * CUDA; flash_gmm_cpu.cpp:292-311 on the CPU).
+ */
+int fgmm_standard_m_step(const float* X, const float* gamma, long N, int K, int d,
+                         float* mu, float* var, float* log_pi, void* ws, size_t ws_bytes,
+                         void* stream);
 
 /*
  * Kernel timing with HIP events recorded on the launch stream around every

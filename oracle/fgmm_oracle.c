@@ -292,7 +292,7 @@ void orc_standard_m_step(const float* X, const double* gamma, long N, int K,
             double m = s[j] / nk;
             double v = sq[j] / nk - m * m;
             s[j] = m;
-            sq[j] = v > 1e-6 ? v : 1e-6;
+            sq[j] = v < 1e-6 ? 1e-6 : v;   /* clamp_min keeps NaN (n = 0) */
         }
         log_pi[k] = log(nk / (double)N);
     }
@@ -433,7 +433,7 @@ void orc32_standard_m_step(const float* X, const float* gamma, long N, int K,
             float m = s[j] / nk;
             float v = sq[j] / nk - m * m;
             s[j] = m;
-            sq[j] = v > 1e-6f ? v : 1e-6f;
+            sq[j] = v < 1e-6f ? 1e-6f : v;   /* clamp_min keeps NaN (n = 0) */
         }
         log_pi[k] = logf(nk / (float)N);
     }

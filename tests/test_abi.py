@@ -29,7 +29,8 @@ def lib():
 def test_header_declares_entry_points():
     names = declared()
     for must in ("fgmm_em_fused", "fgmm_log_normalizer", "fgmm_accumulate_stats",
-                 "fgmm_m_step_update", "fgmm_em_fit", "fgmm_workspace_bytes"):
+                 "fgmm_m_step_update", "fgmm_em_fit", "fgmm_workspace_bytes",
+                 "fgmm_flash_e_step", "fgmm_standard_e_step", "fgmm_standard_m_step"):
         assert must in names
 
 
@@ -64,6 +65,38 @@ def test_workspace_bytes(lib):
             assert b >= 8 * N      # holds the fp64 log-normalizer at least
     assert lib.fgmm_workspace_bytes(0, 8, 32, 0) == 0
     assert lib.fgmm_workspace_bytes(10, 8, 257, 0) == 0
+
+
+def test_estep_workspace_bytes(lib):
+    for N, K, d in ((4096, 8, 32), (65536, 256, 128), (5, 3, 256), (1, 1, 1)):
+        base = lib.fgmm_workspace_bytes(N, K, d, 0)
+        std = lib.fgmm_standard_e_step_workspace_bytes(N, K, d, 0)
+        assert std % 256 == 0 and std >= base + 8 * N * K   # + the fp64 N x K matrix
+        # x32 has no gamma-returning form: it runs as the MFMA path
+        if d <= 128:
+            assert (lib.fgmm_standard_e_step_workspace_bytes(N, K, d, 3)
+                    == lib.fgmm_standard_e_step_workspace_bytes(N, K, d, 2))
+        m = lib.fgmm_standard_m_step_workspace_bytes(N, K, d)
+        assert m > 0 and m % 256 == 0
+    assert lib.fgmm_standard_e_step_workspace_bytes(10, 3, 200, 2) == 0
+    assert lib.fgmm_standard_m_step_workspace_bytes(10, 0, 8) == 0
+    assert lib.fgmm_standard_m_step_workspace_bytes(10, 3, 257) == 0
+
+
+def test_estep_argument_errors(lib):
+    ws = 1 << 30
+    for fn in (lib.fgmm_flash_e_step, lib.fgmm_standard_e_step):
+        assert fn(0x1000, 0x1000, 0x1000, 0x1000, 0, 4, 8, 0, 0x1000, 0x1000, 0x1000, ws,
+                  None) == 1 and b"N must be" in lib.fgmm_last_error()
+        assert fn(0x1000, 0x1000, 0x1000, 0x1000, 10, 4, 8, 0, None, 0x1000, 0x1000, ws,
+                  None) == 1 and b"gamma must not be NULL" in lib.fgmm_last_error()
+        assert fn(0x1000, 0x1000, 0x1000, 0x1000, 10, 4, 8, 0, 0x1000, 0x1000, 0x1000, 64,
+                  None) == 2 and b"too small" in lib.fgmm_last_error()
+    f = lib.fgmm_standard_m_step
+    assert f(0x1000, None, 10, 4, 8, 0x1000, 0x1000, 0x1000, 0x1000, ws, None) == 1
+    assert b"gamma must not be NULL" in lib.fgmm_last_error()
+    assert f(0x1000, 0x1000, 10, 4, 300, 0x1000, 0x1000, 0x1000, 0x1000, ws, None) == 1
+    assert f(0x1000, 0x1000, 10, 4, 8, 0x1000, 0x1000, 0x1000, 0x1001, ws, None) == 2
 
 
 def _em(lib, N=100, K=4, d=8, variant=0, ws=0x1000, wsb=1 << 30, null=None):
@@ -104,6 +137,17 @@ def test_python_errors_mirror_reference():
         C.flash_em_fused(X, mu, var, lp)
     with pytest.raises(RuntimeError, match="BN and BK"):
         C.flash_em_fused(X, mu, var, lp, 0, 8)
+    for fn in (C.standard_e_step, C.flash_e_step):
+        with pytest.raises(RuntimeError, match="X must be float32"):
+            fn(X.double(), mu, var, lp)
+        with pytest.raises(RuntimeError, match="ROCm device"):
+            fn(X, mu, var, lp)
+    with pytest.raises(RuntimeError, match="X must be float32"):
+        C.standard_m_step(X.double(), torch.zeros(10, 2))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        C.standard_m_step(X, torch.zeros(10, 2))
+    with pytest.raises(RuntimeError, match="BK must be"):
+        C.flash_e_step(X, mu, var, lp, BK=0)
     with pytest.raises(RuntimeError, match="unknown variant"):
         from flashgmm_amd import _lib
         _lib.variant_code("fast")
