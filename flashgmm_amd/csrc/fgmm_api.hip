@@ -103,7 +103,6 @@ WsLayout make_layout(const Geom& g) {
     off = align256(off + sizeof(float) * N);                    // m32
     off = align256(off + sizeof(unsigned short) * 8 * N);       // slot components
     off = align256(off + sizeof(float) * 8 * N);                // slot gammas
-    off = align256(off + N);                                    // overflow flags
   }
   L.total = off;
   return L;
@@ -199,17 +198,27 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
     w.x.P32 = reinterpret_cast<const float*>(w.params + 2 * (size_t)g.Kp * g.dp);
     w.x.b64 = w.bias;
     w.x.bias32 = reinterpret_cast<const float*>(w.bias + g.Kp);
-    w.x.exact = reinterpret_cast<const int*>(w.x.bias32 + g.Kp);
+    w.x.Z32 = w.x.bias32 + g.Kp;
     size_t off = L.aux;
     w.x.m32 = reinterpret_cast<float*>(b + off);
     off = align256(off + sizeof(float) * N);
     w.x.ck = reinterpret_cast<unsigned short*>(b + off);
     off = align256(off + sizeof(unsigned short) * 8 * N);
     w.x.cg = reinterpret_cast<float*>(b + off);
-    off = align256(off + sizeof(float) * 8 * N);
-    w.x.ovf = reinterpret_cast<unsigned char*>(b + off);
   }
   return w;
+}
+
+// What the reduction's exact fallback of the x32 variant reads.
+static X32Exact x32_exact(const Geom& g, const float* X, const Ws& w) {
+  X32Exact xa;
+  if (g.variant == kX32) {
+    xa.X = X;
+    xa.ln2 = w.ln2;
+    xa.V = w.params;
+    xa.b64 = w.bias;
+  }
+  return xa;
 }
 
 static int run_precompute(const Geom& g, const float* mu, const float* var,
@@ -236,8 +245,9 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
   return check_hip(e, "pass 2 (sufficient statistics)");
 }
 
-// The gamma-returning E-steps have no x32 form: the candidate scheme pays off
-// only when gamma is consumed on chip, so they run the fp64 matrix-core path.
+// Entry points without an x32 form (the gamma-returning E-steps, whose
+// candidate scheme would pay off only when gamma is consumed on chip, and
+// Pass 2 from a caller's log-normalizer) run the fp64 matrix-core path.
 static int estep_variant(int variant) { return variant == kX32 ? kMfma : variant; }
 
 // Standard E-step workspace: the common regions, then the fp64 matrix L.
@@ -303,7 +313,8 @@ int fgmm_em_fused(const float* X, const float* mu, const float* var, const float
   if ((rc = run_pass2(g, X, w, s))) return rc;
   Timed t(3, s);
   return check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, new_mu,
-                                 new_var, new_log_pi, nullptr, nullptr, nullptr, s),
+                                 new_var, new_log_pi, nullptr, nullptr, nullptr, s, 0,
+                                 x32_exact(g, X, w)),
                    "reduction / M-step");
 }
 
@@ -329,6 +340,9 @@ int fgmm_accumulate_stats(const float* X, const float* mu, const float* var,
                           int d, int variant, float* n_k, float* s_k, float* sq_k, void* ws,
                           size_t ws_bytes, void* stream) {
   g_err[0] = 0;
+  // x32's Pass 2 needs its own Pass 1 (window anchors, slots); with a caller's
+  // log-normalizer the fp64 matrix-core pass runs instead
+  variant = estep_variant(variant);
   int rc = validate_shape(N, K, d, variant);
   if (rc) return rc;
   FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
@@ -385,7 +399,8 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
     // the M-step writes the fp32 parameters and, from their fp32 values, the
     // coefficients the next iteration's passes read
     rc = check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu_out,
-                                 var_out, log_pi_out, w.params, w.bias, ll_traj + it, s),
+                                 var_out, log_pi_out, w.params, w.bias, ll_traj + it, s, 0,
+                                 x32_exact(g, X, w)),
                    "reduction / M-step");
     if (rc) return rc;
   }

@@ -51,12 +51,13 @@ __device__ inline double block_sum_f64(double v, double* red) {
 // m / v are the fp32 parameter values of this component (nullptr for a
 // padding component, which gets zero coefficients and bias -inf).
 // The x32 variant stores the direct-form fp64 set (as VALU) plus an fp32
-// fragment-ordered expanded set behind it, and two biases.
+// fragment-ordered expanded set behind it, two biases and the error constant
+// Z_k of its fp32 distance model (x32_err_c).
 __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
                              const float* m, const float* v, float lp,
                              double* P, double* bias, double* red) {
   const bool real = (m != nullptr);
-  double lnv = 0.0, q = 0.0, cond = 0.0;
+  double lnv = 0.0, q = 0.0;
   const int Q = dp / 4, S1 = dp / 2;
   float* P32 = reinterpret_cast<float*>(P + 2 * (size_t)Kp * dp);
   for (int j = threadIdx.x; j < dp; j += blockDim.x) {
@@ -67,8 +68,6 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
       mu = (double)m[j];
       lnv += log(vv);
       q += mu * mu * iv;
-      const double span = fabs(mu) + 4.0 * sqrt(vv);   // |x| within 4 sigma of mu
-      cond += span * span * iv;
     }
     const int ks = k >> 4, c = k & 15, g = j / Q, t = j - g * Q;
     const int lane = 16 * g + c;
@@ -87,27 +86,24 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
   }
   lnv = block_sum_f64(lnv, red);
   q = block_sum_f64(q, red);
-  if (variant == kX32) cond = block_sum_f64(cond, red);
   if (threadIdx.x == 0) {
     float* bias32 = reinterpret_cast<float*>(bias + Kp);
-    int* exact = reinterpret_cast<int*>(bias32 + Kp);
+    float* Z32 = bias32 + Kp;
     if (!real) {
       bias[k] = -INFINITY;
       if (variant == kX32) {
         bias32[k] = -INFINITY;
-        exact[k] = 0;
+        Z32[k] = 0.f;
       }
     } else {
       double lc = (double)lp - 0.5 * ((double)d * kLog2Pi + lnv);
       bias[k] = (variant == kMfma) ? kLog2e * (lc - 0.5 * q) : kLog2e * lc;
       if (variant == kX32) {
-        bias32[k] = (float)(kLog2e * (lc - 0.5 * q));
-        // Rounding of the fp32 expanded distance for points near this
-        // component: ~ sqrt(2dp) * 2^-24 * log2(e) * sum_j (|mu|+4 sigma)^2/var
-        // bits.  Above 1 bit the component is evaluated exactly for every
-        // point (collapsed components, var -> 1e-6, land here).
-        const double err_bits = sqrt(2.0 * dp) * 5.9604644775390625e-8 * kLog2e * cond;
-        exact[k] = err_bits > 1.0 ? 1 : 0;
+        const double be = kLog2e * (lc - 0.5 * q);
+        bias32[k] = (float)be;
+        // |bias| + D_k, D_k = 0.5 log2(e) sum mu^2/var; rounded up to fp32
+        const double z = x32_err_c(dp) * (fabs(be) + 0.5 * kLog2e * q);
+        Z32[k] = (float)(z * (1.0 + 1e-6));
       }
     }
   }
@@ -141,6 +137,44 @@ hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
 // dp <= f < 2dp -> sum gamma*x_j^2, f = 2dp -> sum gamma.  Sums over s run in fp64 in a fixed
 // order, so results are bitwise reproducible.
 // ---------------------------------------------------------------------------
+// x32 variant: the fp32 responsibilities of pairs outside the exact window
+// carry a per-pair error bound; Pass 2 sums these bounds per component into
+// column 2dp+1 of the partial row.  When the bound reaches kX32Guard of the
+// component's (clamped) mass -- a component whose mass lies almost entirely
+// in pairs far below every point's best component -- its statistics are
+// recomputed here exactly (fp64 log-density and responsibility for every
+// point; blockDim.x >= d, which holds as x32 requires d <= 128).
+constexpr double kX32Guard = 1e-7;
+
+__device__ void exact_component_stats(int k, long N, int d, int Kp, int dp,
+                                      const X32Exact& xa, double& a, double& b,
+                                      double& nk, double* red) {
+  __shared__ double gsh[128];
+  const int tid = threadIdx.x;
+  double sa = 0.0, sb = 0.0, sn = 0.0;
+  for (long n0 = 0; n0 < N; n0 += 128) {
+    const long n = n0 + tid;
+    double gam = 0.0;
+    if (tid < 128 && n < N)
+      gam = exp2(exact_ll2(xa.X + (size_t)n * d, d, xa.V, Kp, dp, xa.b64, k) - xa.ln2[n]);
+    sn += gam;
+    __syncthreads();
+    if (tid < 128) gsh[tid] = gam;
+    __syncthreads();
+    if (tid < d) {
+      const long cnt = (N - n0 < 128) ? N - n0 : 128;
+      for (int i = 0; i < cnt; i++) {
+        const double x = (double)xa.X[(size_t)(n0 + i) * d + tid];
+        sa = fma(gsh[i], x, sa);
+        sb = fma(gsh[i], x * x, sb);
+      }
+    }
+  }
+  nk = block_sum_f64(sn, red);
+  a = sa;
+  b = sb;
+}
+
 __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               int S, int stat_w, const double* __restrict__ part,
                               const double* __restrict__ lnsum, int n_lnsum,
@@ -149,9 +183,10 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               float* __restrict__ new_var,
                               float* __restrict__ new_log_pi,
                               double* __restrict__ P_next, double* __restrict__ bias_next,
-                              double* __restrict__ ll_out, int standard) {
+                              double* __restrict__ ll_out, int standard, X32Exact xa) {
   __shared__ double red[16];
   __shared__ double nk_sh;
+  __shared__ int exact_sh;
   __shared__ float mu_sh[kMaxD], var_sh[kMaxD];
   const int k = blockIdx.x;
 
@@ -176,18 +211,39 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     const double* p = part + (size_t)k * row + 2 * dp;
     for (int s = threadIdx.x; s < S; s += blockDim.x) t += p[(size_t)s * kstride];
     t = block_sum_f64(t, red);
-    if (threadIdx.x == 0) nk_sh = t;
+    double eb = 0.0;
+    if (variant == kX32) {
+      for (int s = threadIdx.x; s < S; s += blockDim.x) eb += p[(size_t)s * kstride + 1];
+      eb = block_sum_f64(eb, red);
+    }
+    if (threadIdx.x == 0) {
+      nk_sh = t;
+      exact_sh = (variant == kX32 && eb > kX32Guard * (t > 1e-8 ? t : 1e-8)) ? 1 : 0;
+    }
   }
   __syncthreads();
+  const bool exact = exact_sh != 0;
+  double ea = 0.0, eb2 = 0.0;
+  if (exact) {
+    double enk;
+    exact_component_stats(k, N, d, Kp, dp, xa, ea, eb2, enk, red);
+    if (threadIdx.x == 0) nk_sh = enk;
+    __syncthreads();
+  }
   const double nk = nk_sh;
   const double inv = standard ? 1.0 / nk : 1.0 / (nk > 1e-8 ? nk : 1e-8);
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
     double a = 0.0, b = 0.0;
     const double* p = part + (size_t)k * row;
+    if (exact) {
+      a = ea;
+      b = eb2;
+    } else {
 #pragma unroll 8
-    for (int s = 0; s < S; s++) {
-      a += p[(size_t)s * kstride + j];
-      b += p[(size_t)s * kstride + dp + j];
+      for (int s = 0; s < S; s++) {
+        a += p[(size_t)s * kstride + j];
+        b += p[(size_t)s * kstride + dp + j];
+      }
     }
     if (s_k != nullptr) {
       s_k[(size_t)k * d + j] = (float)a;
@@ -222,12 +278,16 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
 hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
-                         double* bias_next, double* ll_out, hipStream_t s, int standard) {
+                         double* bias_next, double* ll_out, hipStream_t s, int standard,
+                         X32Exact xa) {
+  if (g.variant == kX32 && (xa.X == nullptr || xa.ln2 == nullptr || xa.V == nullptr ||
+                            xa.b64 == nullptr || g.d > 128))
+    return hipErrorInvalidValue;
   const int blocks = params_next != nullptr ? g.Kp : g.K;
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
-                     bias_next, ll_out, standard);
+                     bias_next, ll_out, standard, xa);
   return hipGetLastError();
 }
 

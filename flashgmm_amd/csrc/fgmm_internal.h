@@ -58,26 +58,55 @@ struct WsLayout {
   size_t ln2;       // fp64 [N]   base-2 log-normalizer
   size_t lnsum;     // fp64 [p1_blocks] per-workgroup sums of ln (natural)
   size_t part;      // fp64 [S][Kp][stat_w] sufficient-statistic partials
-  size_t aux;       // x32 only: fp32 max ll [N], candidate slots [N][8]
-                    // (u16 component, fp32 gamma), overflow flags [N]
+  size_t aux;       // x32 only: fp32 window anchor [N], candidate slots [N][8]
+                    // (u16 component, fp32 gamma)
   size_t total;
 };
 
 // Coefficient views of the x32 variant (see fgmm_x32.hip).  The params
 // region holds the fp64 direct-form coefficients V (same layout as the VALU
 // variant) followed by the fp32 fragment-ordered coefficients; the bias
-// region holds the fp64 direct-form bias followed by the fp32 expanded bias.
+// region holds the fp64 direct-form bias, the fp32 expanded bias and the
+// fp32 per-component error constants Z.
 struct X32Ws {
   const float* P32;
   const float* bias32;
-  const int* exact;   // [Kp] 1 = evaluate this component exactly for every point
+  const float* Z32;
   const double* V;
   const double* b64;
-  float* m32;
-  unsigned short* ck;
-  float* cg;
-  unsigned char* ovf;
+  float* m32;          // [N]  max over k of the lower bound ll32 - E (log2 units)
+  unsigned short* ck;  // [N][8] slot components (0xFFFF = empty)
+  float* cg;           // [N][8] slot responsibilities (exact)
 };
+
+// Error model of the fp32 expanded distance (x32 variant).  ll32 is
+// fl(a0 + a1) with a0 = sum_j P1_kj x_j^2 and a1 = bias_k + sum_j P2_kj x_j
+// accumulated in fp32 on the matrix cores from fp32-rounded P1, P2, bias and
+// x^2.  Every rounding is relative 2^-24 of a partial sum bounded by
+// sum |terms| = |bias_k| + sum|P1 x^2| + sum|P2 x|, and with P2 = -2 mu P1
+// (P1 < 0), |P2 x| <= |P1| (mu^2 + x^2), so
+//     |ll32 - ll2| <= c * (|bias_k| + D_k + 2 |a0|),  D_k = sum_j |P1_kj| mu_kj^2
+// with c = (2 dp + 8) 2^-24 (dp + 1 chained additions per accumulator, four
+// input roundings, the final add; doubled for margin).  Z_k = c (|bias_k| +
+// D_k) is precomputed per component; the slope on |a0| is 2c.
+constexpr double kU32 = 5.9604644775390625e-8;  // 2^-24
+__host__ __device__ constexpr double x32_err_c(int dp) { return (2.0 * dp + 8.0) * kU32; }
+
+// Exact base-2 log-density of row x (fp32, length d) under component k from
+// the fp64 direct-form coefficients (VALU layout: V[k*dp + j] = s_kj,
+// V[Kp*dp + k*dp + j] = mu_kj s_kj, b64[k] = log2(e) log_coeff_k).
+__device__ inline double exact_ll2(const float* __restrict__ x, int d,
+                                   const double* __restrict__ V, int Kp, int dp,
+                                   const double* __restrict__ b64, int k) {
+  const double* S = V + (size_t)k * dp;
+  const double* MS = V + (size_t)Kp * dp + (size_t)k * dp;
+  double acc = 0.0;
+  for (int j = 0; j < d; j++) {
+    const double t = fma((double)x[j], S[j], -MS[j]);
+    acc = fma(t, t, acc);
+  }
+  return b64[k] - acc;
+}
 
 Geom make_geom(long N, int K, int d, int variant);
 WsLayout make_layout(const Geom& g);
@@ -98,11 +127,20 @@ hipError_t launch_pass2(const Geom& g, const float* X, const double* params,
 // and ll_out = sum(lnsum)/N.
 // standard != 0 selects the standard M-step's arithmetic (no clamp on n_k or
 // n_k/N); the variance floor 1e-6 applies to both.
+// For the x32 variant `xa` carries what the exact fallback of a component
+// needs (see reduce_kernel): X, the fp64 log-normalizer and the current
+// direct-form coefficients.
+struct X32Exact {
+  const float* X = nullptr;
+  const double* ln2 = nullptr;
+  const double* V = nullptr;
+  const double* b64 = nullptr;
+};
 hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s,
-                         int standard = 0);
+                         int standard = 0, X32Exact xa = X32Exact());
 // Pass-1 sweep in one of the Sweep modes (the MFMA or VALU kernels by
 // g.variant).  kSweepGamma reads ln2 and writes gamma [N][K] (fp32);
 // kSweepLL writes Lmat [N][K] (fp64, base 2).
