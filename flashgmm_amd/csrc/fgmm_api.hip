@@ -54,7 +54,7 @@ Geom make_geom(long N, int K, int d, int variant) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
     g.p1_blocks = (int)((N + 127) / 128);
-    g.p2_kblocks = (g.Kp / 16 + 3) / 4;
+    g.p2_kblocks = (g.Kp / 16 + 3) / 4;   // Pass-2 workgroup: 4 x 16 components
   } else {
     int dp = 16;
     while (dp < d) dp <<= 1;
@@ -101,8 +101,10 @@ WsLayout make_layout(const Geom& g) {
   if (x32) {
     const size_t N = (size_t)g.N;
     off = align256(off + sizeof(float) * N);                    // m32
-    off = align256(off + sizeof(unsigned short) * 8 * N);       // slot components
-    off = align256(off + sizeof(float) * 8 * N);                // slot gammas
+    off = align256(off + sizeof(float) * N);                    // max x^2
+    off = align256(off + sizeof(unsigned short) * kX32Slots * N);   // slot components
+    off = align256(off + sizeof(float) * kX32Slots * N);        // slot gammas
+    off = align256(off + sizeof(int) * (size_t)g.Kp);           // exact-fix flags
   }
   L.total = off;
   return L;
@@ -185,13 +187,14 @@ struct Ws {
   double* lnsum;
   double* part;
   X32Ws x;
+  bool layout_ok;
 };
 
 static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
   char* b = static_cast<char*>(ws);
   Ws w{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
        reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
-       reinterpret_cast<double*>(b + L.part), X32Ws{}};
+       reinterpret_cast<double*>(b + L.part), X32Ws{}, true};
   if (g.variant == kX32) {
     const size_t N = (size_t)g.N;
     w.x.V = w.params;
@@ -202,23 +205,40 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
     size_t off = L.aux;
     w.x.m32 = reinterpret_cast<float*>(b + off);
     off = align256(off + sizeof(float) * N);
+    w.x.xm = reinterpret_cast<float*>(b + off);
+    off = align256(off + sizeof(float) * N);
     w.x.ck = reinterpret_cast<unsigned short*>(b + off);
-    off = align256(off + sizeof(unsigned short) * 8 * N);
+    off = align256(off + sizeof(unsigned short) * kX32Slots * N);
     w.x.cg = reinterpret_cast<float*>(b + off);
+    off = align256(off + sizeof(float) * kX32Slots * N);
+    w.x.flag = reinterpret_cast<int*>(b + off);
+    off = align256(off + sizeof(int) * (size_t)g.Kp);
+    w.layout_ok = (off == L.total);   // the carve must end where the layout does
   }
   return w;
 }
 
-// What the reduction's exact fallback of the x32 variant reads.
-static X32Exact x32_exact(const Geom& g, const float* X, const Ws& w) {
-  X32Exact xa;
-  if (g.variant == kX32) {
-    xa.X = X;
-    xa.ln2 = w.ln2;
-    xa.V = w.params;
-    xa.b64 = w.bias;
-  }
-  return xa;
+// Reduction + M-step of one iteration.  x32: stage 1 reduces the components
+// whose fp32-responsibility error bounds are negligible and flags the rest,
+// their partials are recomputed exactly, stage 2 finishes them.
+static int run_reduce(const Geom& g, const float* X, Ws& w, float* mu, float* var, float* lp,
+                      double* params_next, double* bias_next, double* ll_out, hipStream_t s) {
+  Timed t(3, s);
+  if (g.variant != kX32)
+    return check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu, var, lp,
+                                   params_next, bias_next, ll_out, s),
+                     "reduction / M-step");
+  int rc = check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu, var, lp,
+                                   params_next, bias_next, ll_out, s, 0, kReduceFlagging,
+                                   w.x.flag),
+                     "reduction / M-step");
+  if (rc) return rc;
+  rc = check_hip(launch_x32_fix(g, X, w.x, w.ln2, w.part, s), "exact statistics (x32)");
+  if (rc) return rc;
+  return check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu, var, lp,
+                                 params_next, bias_next, nullptr, s, 0, kReduceFlagged,
+                                 w.x.flag),
+                   "reduction / M-step (exact components)");
 }
 
 static int run_precompute(const Geom& g, const float* mu, const float* var,
@@ -228,6 +248,7 @@ static int run_precompute(const Geom& g, const float* mu, const float* var,
 }
 
 static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStream_t s) {
+  if (!w.layout_ok) return fail(FGMM_EWORKSPACE, "internal: workspace carve does not match its layout");
   Timed t(1, s);
   hipError_t e =
       g.variant == kMfma  ? launch_pass1_mfma(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s)
@@ -311,11 +332,7 @@ int fgmm_em_fused(const float* X, const float* mu, const float* var, const float
   if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
   if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
   if ((rc = run_pass2(g, X, w, s))) return rc;
-  Timed t(3, s);
-  return check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, new_mu,
-                                 new_var, new_log_pi, nullptr, nullptr, nullptr, s, 0,
-                                 x32_exact(g, X, w)),
-                   "reduction / M-step");
+  return run_reduce(g, X, w, new_mu, new_var, new_log_pi, nullptr, nullptr, nullptr, s);
 }
 
 int fgmm_log_normalizer(const float* X, const float* mu, const float* var,
@@ -395,13 +412,9 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
   for (int it = 0; it < iters; it++) {
     if ((rc = run_pass1(g, X, w, nullptr, s))) return rc;
     if ((rc = run_pass2(g, X, w, s))) return rc;
-    Timed t(3, s);
     // the M-step writes the fp32 parameters and, from their fp32 values, the
     // coefficients the next iteration's passes read
-    rc = check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu_out,
-                                 var_out, log_pi_out, w.params, w.bias, ll_traj + it, s, 0,
-                                 x32_exact(g, X, w)),
-                   "reduction / M-step");
+    rc = run_reduce(g, X, w, mu_out, var_out, log_pi_out, w.params, w.bias, ll_traj + it, s);
     if (rc) return rc;
   }
   return FGMM_OK;

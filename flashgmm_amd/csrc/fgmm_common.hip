@@ -27,6 +27,8 @@ namespace fgmm {
 // VALU layout: P[k*dp + j] = s_kj = sqrt(0.5*log2(e)/var_kj),
 //              P[Kp*dp + k*dp + j] = mu_kj*s_kj,  bias_k = log2(e)*log_coeff_k
 // so that ll2_nk = bias_k - sum_j (x_j*s_kj - mu_kj*s_kj)^2.
+// x32 layout: the same pair interleaved, P[2(k*dp + j)] = s_kj,
+//             P[2(k*dp + j) + 1] = mu_kj*s_kj (one 16-byte load per feature).
 // ---------------------------------------------------------------------------
 
 __device__ inline double wave_sum_f64(double v) {
@@ -74,6 +76,10 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
     if (variant == kMfma) {
       P[((size_t)ks * S1 + t) * 64 + lane] = -0.5 * kLog2e * iv;
       P[((size_t)ks * S1 + Q + t) * 64 + lane] = kLog2e * mu * iv;
+    } else if (variant == kX32) {
+      double sc = sqrt(0.5 * kLog2e * iv);
+      P[2 * ((size_t)k * dp + j)] = sc;
+      P[2 * ((size_t)k * dp + j) + 1] = mu * sc;
     } else {
       double sc = sqrt(0.5 * kLog2e * iv);
       P[(size_t)k * dp + j] = sc;
@@ -137,43 +143,19 @@ hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
 // dp <= f < 2dp -> sum gamma*x_j^2, f = 2dp -> sum gamma.  Sums over s run in fp64 in a fixed
 // order, so results are bitwise reproducible.
 // ---------------------------------------------------------------------------
-// x32 variant: the fp32 responsibilities of pairs outside the exact window
-// carry a per-pair error bound; Pass 2 sums these bounds per component into
-// column 2dp+1 of the partial row.  When the bound reaches kX32Guard of the
-// component's (clamped) mass -- a component whose mass lies almost entirely
-// in pairs far below every point's best component -- its statistics are
-// recomputed here exactly (fp64 log-density and responsibility for every
-// point; blockDim.x >= d, which holds as x32 requires d <= 128).
-constexpr double kX32Guard = 1e-7;
-
-__device__ void exact_component_stats(int k, long N, int d, int Kp, int dp,
-                                      const X32Exact& xa, double& a, double& b,
-                                      double& nk, double* red) {
-  __shared__ double gsh[128];
-  const int tid = threadIdx.x;
-  double sa = 0.0, sb = 0.0, sn = 0.0;
-  for (long n0 = 0; n0 < N; n0 += 128) {
-    const long n = n0 + tid;
-    double gam = 0.0;
-    if (tid < 128 && n < N)
-      gam = exp2(exact_ll2(xa.X + (size_t)n * d, d, xa.V, Kp, dp, xa.b64, k) - xa.ln2[n]);
-    sn += gam;
-    __syncthreads();
-    if (tid < 128) gsh[tid] = gam;
-    __syncthreads();
-    if (tid < d) {
-      const long cnt = (N - n0 < 128) ? N - n0 : 128;
-      for (int i = 0; i < cnt; i++) {
-        const double x = (double)xa.X[(size_t)(n0 + i) * d + tid];
-        sa = fma(gsh[i], x, sa);
-        sb = fma(gsh[i], x * x, sb);
-      }
-    }
-  }
-  nk = block_sum_f64(sn, red);
-  a = sa;
-  b = sb;
-}
+// x32 variant: Pass 2 takes the fp32 responsibility for pairs outside the
+// exact window and sums, per component and point chunk, bounds on the error
+// this puts into its statistics (partial columns after sum gamma):
+//   2dp+1  eb = sum gamma (2^E - 1)              bounds |d sum gamma|
+//   2dp+2  es = sum eb_n max_j |x_nj|            bounds |d sum gamma x_j|
+//   2dp+3  eq = sum eb_n max_j x_nj^2            bounds |d sum gamma x_j^2|
+// Stage kReduceFlagging propagates them to first order through the M-step,
+//   |d mu|  <= (es + |mu| eb) / n,
+//   |d var| <= (eq + (sq/n) eb + 2|mu| (es + |mu| eb)) / n,
+//   |d log n| <= eb / n,                 n = max(n_k, 1e-8),
+// and flags the component when any bound exceeds kX32Guard (a tenth of the
+// 1e-5 parity bar); its statistics are then recomputed exactly.
+constexpr double kX32Guard = 1e-6;
 
 __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               int S, int stat_w, const double* __restrict__ part,
@@ -183,13 +165,17 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               float* __restrict__ new_var,
                               float* __restrict__ new_log_pi,
                               double* __restrict__ P_next, double* __restrict__ bias_next,
-                              double* __restrict__ ll_out, int standard, X32Exact xa) {
+                              double* __restrict__ ll_out, int standard, int stage,
+                              int* __restrict__ flag) {
   __shared__ double red[16];
   __shared__ double nk_sh;
-  __shared__ int exact_sh;
+  __shared__ double errb_sh[3];
+  __shared__ int bad_sh;
   __shared__ float mu_sh[kMaxD], var_sh[kMaxD];
+  __shared__ double sa_sh[kMaxD], sb_sh[kMaxD];
   const int k = blockIdx.x;
 
+  if (stage == kReduceFlagged && (k >= K || flag[k] == 0)) return;
   if (k == 0 && ll_out != nullptr) {
     double t = 0.0;
     for (int i = threadIdx.x; i < n_lnsum; i += blockDim.x) t += lnsum[i];
@@ -198,6 +184,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   }
 
   if (k >= K) {  // padding components only need coefficients for the next pass
+    if (stage == kReduceFlagging && threadIdx.x == 0) flag[k] = 0;
     if (P_next != nullptr)
       write_coeffs(variant, k, Kp, d, dp, nullptr, nullptr, 0.f, P_next, bias_next, red);
     return;
@@ -211,40 +198,49 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     const double* p = part + (size_t)k * row + 2 * dp;
     for (int s = threadIdx.x; s < S; s += blockDim.x) t += p[(size_t)s * kstride];
     t = block_sum_f64(t, red);
-    double eb = 0.0;
-    if (variant == kX32) {
-      for (int s = threadIdx.x; s < S; s += blockDim.x) eb += p[(size_t)s * kstride + 1];
-      eb = block_sum_f64(eb, red);
+    if (stage == kReduceFlagging) {
+      for (int c = 1; c <= 3; c++) {
+        double e = 0.0;
+        for (int s = threadIdx.x; s < S; s += blockDim.x) e += p[(size_t)s * kstride + c];
+        e = block_sum_f64(e, red);
+        if (threadIdx.x == 0) errb_sh[c - 1] = e;
+      }
     }
     if (threadIdx.x == 0) {
       nk_sh = t;
-      exact_sh = (variant == kX32 && eb > kX32Guard * (t > 1e-8 ? t : 1e-8)) ? 1 : 0;
+      bad_sh = 0;
     }
   }
   __syncthreads();
-  const bool exact = exact_sh != 0;
-  double ea = 0.0, eb2 = 0.0;
-  if (exact) {
-    double enk;
-    exact_component_stats(k, N, d, Kp, dp, xa, ea, eb2, enk, red);
-    if (threadIdx.x == 0) nk_sh = enk;
-    __syncthreads();
-  }
   const double nk = nk_sh;
   const double inv = standard ? 1.0 / nk : 1.0 / (nk > 1e-8 ? nk : 1e-8);
+  const double ncl = nk > 1e-8 ? nk : 1e-8;
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
     double a = 0.0, b = 0.0;
     const double* p = part + (size_t)k * row;
-    if (exact) {
-      a = ea;
-      b = eb2;
-    } else {
 #pragma unroll 8
-      for (int s = 0; s < S; s++) {
-        a += p[(size_t)s * kstride + j];
-        b += p[(size_t)s * kstride + dp + j];
-      }
+    for (int s = 0; s < S; s++) {
+      a += p[(size_t)s * kstride + j];
+      b += p[(size_t)s * kstride + dp + j];
     }
+    sa_sh[j] = a;
+    sb_sh[j] = b;
+    if (stage == kReduceFlagging) {
+      const double eb = errb_sh[0], es = errb_sh[1], eq = errb_sh[2];
+      const double m = fabs(a) / ncl, q = fabs(b) / ncl;
+      const double dmu = (es + m * eb) / ncl;
+      const double dvar = (eq + q * eb + 2.0 * m * (es + m * eb)) / ncl;
+      if (dmu > kX32Guard || dvar > kX32Guard || eb / ncl > kX32Guard) bad_sh = 1;
+    }
+  }
+  __syncthreads();
+  if (stage == kReduceFlagging) {
+    const bool bad = bad_sh != 0;
+    if (threadIdx.x == 0) flag[k] = bad ? 1 : 0;
+    if (bad) return;   // statistics recomputed exactly, then reduced in stage 2
+  }
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    const double a = sa_sh[j], b = sb_sh[j];
     if (s_k != nullptr) {
       s_k[(size_t)k * d + j] = (float)a;
       sq_k[(size_t)k * d + j] = (float)b;
@@ -279,15 +275,15 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s, int standard,
-                         X32Exact xa) {
-  if (g.variant == kX32 && (xa.X == nullptr || xa.ln2 == nullptr || xa.V == nullptr ||
-                            xa.b64 == nullptr || g.d > 128))
+                         int stage, int* flag) {
+  if (stage != kReduceAll && (flag == nullptr || g.variant != kX32 || g.stat_w < 2 * g.dp + 4))
     return hipErrorInvalidValue;
-  const int blocks = params_next != nullptr ? g.Kp : g.K;
+  // stage 1 also clears the flags of padding components
+  const int blocks = (params_next != nullptr || stage == kReduceFlagging) ? g.Kp : g.K;
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
-                     bias_next, ll_out, standard, xa);
+                     bias_next, ll_out, standard, stage, flag);
   return hipGetLastError();
 }
 

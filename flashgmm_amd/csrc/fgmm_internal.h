@@ -58,16 +58,16 @@ struct WsLayout {
   size_t ln2;       // fp64 [N]   base-2 log-normalizer
   size_t lnsum;     // fp64 [p1_blocks] per-workgroup sums of ln (natural)
   size_t part;      // fp64 [S][Kp][stat_w] sufficient-statistic partials
-  size_t aux;       // x32 only: fp32 window anchor [N], candidate slots [N][8]
-                    // (u16 component, fp32 gamma)
+  size_t aux;       // x32 only: fp32 window anchor [N], max x^2 [N], candidate
+                    // slots [N][kX32Slots] (u16 component, fp32 gamma), flags [Kp]
   size_t total;
 };
 
 // Coefficient views of the x32 variant (see fgmm_x32.hip).  The params
-// region holds the fp64 direct-form coefficients V (same layout as the VALU
-// variant) followed by the fp32 fragment-ordered coefficients; the bias
-// region holds the fp64 direct-form bias, the fp32 expanded bias and the
-// fp32 per-component error constants Z.
+// region holds the fp64 direct-form coefficients V2 (interleaved pairs
+// V2[k*dp + j] = (s_kj, mu_kj s_kj)) followed by the fp32 fragment-ordered
+// coefficients; the bias region holds the fp64 direct-form bias, the fp32
+// expanded bias and the fp32 per-component error constants Z.
 struct X32Ws {
   const float* P32;
   const float* bias32;
@@ -75,9 +75,12 @@ struct X32Ws {
   const double* V;
   const double* b64;
   float* m32;          // [N]  max over k of the lower bound ll32 - E (log2 units)
-  unsigned short* ck;  // [N][8] slot components (0xFFFF = empty)
-  float* cg;           // [N][8] slot responsibilities (exact)
+  float* xm;           // [N]  max_j x_nj^2
+  unsigned short* ck;  // [N][kX32Slots] slot components (0xFFFF = empty)
+  float* cg;           // [N][kX32Slots] slot responsibilities (exact)
+  int* flag;           // [Kp] components whose statistics are recomputed exactly
 };
+constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
 
 // Error model of the fp32 expanded distance (x32 variant).  ll32 is
 // fl(a0 + a1) with a0 = sum_j P1_kj x_j^2 and a1 = bias_k + sum_j P2_kj x_j
@@ -92,20 +95,27 @@ struct X32Ws {
 constexpr double kU32 = 5.9604644775390625e-8;  // 2^-24
 __host__ __device__ constexpr double x32_err_c(int dp) { return (2.0 * dp + 8.0) * kU32; }
 
-// Exact base-2 log-density of row x (fp32, length d) under component k from
-// the fp64 direct-form coefficients (VALU layout: V[k*dp + j] = s_kj,
-// V[Kp*dp + k*dp + j] = mu_kj s_kj, b64[k] = log2(e) log_coeff_k).
-__device__ inline double exact_ll2(const float* __restrict__ x, int d,
-                                   const double* __restrict__ V, int Kp, int dp,
-                                   const double* __restrict__ b64, int k) {
-  const double* S = V + (size_t)k * dp;
-  const double* MS = V + (size_t)Kp * dp + (size_t)k * dp;
+// sum_{j in [j0, j1)} (x_j s_kj - mu_kj s_kj)^2 in fp64 from the interleaved
+// direct-form coefficients of the x32 variant (V2 pairs, see X32Ws).
+__device__ inline double x32_dist(const float* __restrict__ x, int j0, int j1,
+                                  const double* __restrict__ V2, int dp, int k) {
+  const double2* c = reinterpret_cast<const double2*>(V2) + (size_t)k * dp;
   double acc = 0.0;
-  for (int j = 0; j < d; j++) {
-    const double t = fma((double)x[j], S[j], -MS[j]);
+#pragma unroll 4
+  for (int j = j0; j < j1; j++) {
+    const double2 sm = c[j];
+    const double t = fma((double)x[j], sm.x, -sm.y);
     acc = fma(t, t, acc);
   }
-  return b64[k] - acc;
+  return acc;
+}
+
+// Exact base-2 log-density of row x (fp32, length d) under component k
+// (b64[k] = log2(e) log_coeff_k).
+__device__ inline double exact_ll2(const float* __restrict__ x, int d,
+                                   const double* __restrict__ V2, int dp,
+                                   const double* __restrict__ b64, int k) {
+  return b64[k] - x32_dist(x, 0, d, V2, dp, k);
 }
 
 Geom make_geom(long N, int K, int d, int variant);
@@ -130,17 +140,19 @@ hipError_t launch_pass2(const Geom& g, const float* X, const double* params,
 // For the x32 variant `xa` carries what the exact fallback of a component
 // needs (see reduce_kernel): X, the fp64 log-normalizer and the current
 // direct-form coefficients.
-struct X32Exact {
-  const float* X = nullptr;
-  const double* ln2 = nullptr;
-  const double* V = nullptr;
-  const double* b64 = nullptr;
-};
+// x32: the reduction runs twice per iteration.  Stage 1 (flag != nullptr)
+// writes flag[k] = 1 for components whose fp32-responsibility error bound is
+// not negligible and leaves them alone; launch_x32_fix then overwrites their
+// partials with exact ones and stage 2 reduces only the flagged components.
+enum ReduceStage : int { kReduceAll = 0, kReduceFlagging = 1, kReduceFlagged = 2 };
 hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* n_k, float* s_k, float* sq_k, float* new_mu,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s,
-                         int standard = 0, X32Exact xa = X32Exact());
+                         int standard = 0, int stage = kReduceAll, int* flag = nullptr);
+// Exact partials [chunk][k][*] of the flagged components (x32).
+hipError_t launch_x32_fix(const Geom& g, const float* X, const X32Ws& w, const double* ln2,
+                          double* part, hipStream_t s);
 // Pass-1 sweep in one of the Sweep modes (the MFMA or VALU kernels by
 // g.variant).  kSweepGamma reads ln2 and writes gamma [N][K] (fp32);
 // kSweepLL writes Lmat [N][K] (fp64, base 2).

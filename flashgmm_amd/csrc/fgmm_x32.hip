@@ -9,25 +9,29 @@
 //     E_nk = Z_k + 2c |a0_nk|          (x32_err_c, fgmm_internal.h)
 // from its own accumulator a0 = sum_j P1_kj x_j^2, so only pairs whose upper
 // bound ll32 + E reaches into a window of kWin bits below the point's best
-// lower bound are evaluated exactly (fp64 direct form on the vector ALU):
+// lower bound are evaluated exactly (fp64 direct form):
 //
 //   Pass 1  per point: running M = max_k (ll32 - E) (merged across the four
-//           lane groups every tile); a pair with ll32 + E >= M - kWin joins
-//           the lane's pending list, entries that fall out of the window as
-//           M rises are dropped, survivors are evaluated exactly at the end
-//           (a full list evaluates the newcomer at once).  ln2 is the exact
-//           log-sum-exp of the evaluated pairs; every other pair lies more
-//           than kWin = 40 bits below the maximum, so the omitted mass is
-//           below K 2^-40 relative.  Each lane keeps its two largest exact
-//           pairs as slots (component, gamma) for Pass 2.
+//           lane groups every tile); a pair with ll32 + E >= M - kWin goes to
+//           its lane's pending list in LDS.  When a list could overflow, and
+//           at the end of the sweep, the pending pairs still inside the window
+//           are evaluated cooperatively: the four lanes of a point each hold
+//           a quarter of its features in registers, compute that quarter of
+//           the fp64 distance and combine with two shuffles.  ln2 is the
+//           exact log-sum-exp of the evaluated pairs; every other pair lies
+//           more than kWin = 40 bits below the maximum, so the omitted mass
+//           is below K 2^-40 relative.  Each lane keeps its four largest
+//           exact pairs as slots (component, gamma) for Pass 2.
 //   Pass 2  fp32 GEMM1 -> ll32 and E.  Window pairs take gamma from the slots
-//           (or recompute it exactly when absent); all other pairs take
-//           exp2(ll32 - ln2) and add their error bound gamma (2^E - 1) to a
-//           per-component sum.  The statistics products are those of the
-//           fp64 variant (sum gamma x on fp32 MFMA, sum gamma x^2 on fp64).
-//           The reduction recomputes a component exactly when that error sum
-//           is not negligible against its mass (components starved of
-//           responsibility, whose mass all lies in far-below-window pairs).
+//           (recomputed exactly if absent); all other pairs take
+//           exp2(ll32 - ln2) and add bounds on the error this puts into
+//           n_k, sum gamma x and sum gamma x^2 to per-component sums.  The
+//           statistics products are those of the fp64 variant.
+//   Fix     the reduction flags components whose bounds could move mu, var
+//           or log pi by more than a tenth of the parity bar (components
+//           starved of responsibility, whose mass lies in far-below-window
+//           pairs); x32_fix_kernel recomputes their partials exactly and a
+//           second reduction stage finishes them.
 //
 // Reference kernels these replace (file:line in the reference repository):
 //   Pass 1  flash_log_normalizer_v2_kernel    flash_gmm/csrc/flash_gmm_cuda.cu:72-170
@@ -47,11 +51,13 @@ constexpr int kW1 = 8;                  // Pass 1 wavefronts per workgroup
 constexpr int kPts1 = 16 * kW1;         // Pass 1 points per workgroup
 constexpr int kThr1 = 64 * kW1;
 constexpr int kSub1 = 2;                // 16-component subtiles per LDS tile
-constexpr int kPend = 4;                // pending window pairs per lane
+constexpr int kPendL = 16;              // pending list length per lane (>= 8 per tile)
 constexpr int kW2 = 4;                  // Pass 2 wavefronts (16 components each)
+constexpr int kThr2 = 64 * kW2;
 constexpr int kTile2 = 64;              // Pass 2 points per LDS tile
 constexpr float kWin = 40.0f;           // exact window, log2 units
-constexpr int kSlots = 8;               // slots per point (2 per lane group)
+constexpr int kSlots = kX32Slots;       // slots per point (4 per lane group)
+static_assert(kSlots == 16, "Pass 1 writes 4 slots per lane group, Pass 2 reads 2 x uint4");
 constexpr unsigned short kNoSlot = 0xFFFF;
 
 __device__ inline f32x4 mfma32(float a, float b, f32x4 c) {
@@ -84,32 +90,40 @@ __device__ inline void load_quarter32(const float* __restrict__ X, long n, long 
 // Pass 1.  Workgroup = 8 wavefronts x 16 points, coefficient tiles of 32
 // components double-buffered in LDS (as the fp64 variant).  The fp32
 // accumulator of the 16x16x4 instruction gives lane (g, c) components 4g+r
-// (r = 0..3) of each subtile for point c.
+// (r = 0..3) of each subtile for point c; the same lane holds features
+// [gQ, (g+1)Q) of point c.  Behind the two coefficient tiles LDS holds the
+// lanes' pending lists, entry i of thread t at i*512 + t (conflict-free).
 // ---------------------------------------------------------------------------
 template <int DP, bool VEC>
 __global__ __launch_bounds__(512) void pass1_x32_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const float* __restrict__ P32,
     const float* __restrict__ bias32, const float* __restrict__ Z32,
-    const double* __restrict__ V, const double* __restrict__ b64,
+    const double* __restrict__ V2, const double* __restrict__ b64,
     double* __restrict__ ln2, float* __restrict__ ln_out, double* __restrict__ lnsum,
-    float* __restrict__ m32, unsigned short* __restrict__ ck, float* __restrict__ cg) {
+    float* __restrict__ m32, float* __restrict__ xm, unsigned short* __restrict__ ck,
+    float* __restrict__ cg) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int TILE = kSub1 * S1 * 64;                 // floats per K tile
   constexpr int TV4 = TILE / 4;                         // float4 per tile
   constexpr int PER = (TV4 + kThr1 - 1) / kThr1;
   constexpr float Wslope = (float)(2.0 * x32_err_c(DP));
-  extern __shared__ float smemf[];                      // [2][TILE]
+  extern __shared__ float smemf[];                      // [2][TILE], int2 [kPendL][512]
   __shared__ float sB[2][16 * kSub1], sZ[2][16 * kSub1];
   __shared__ double red[kW1];
+  int2* plist = reinterpret_cast<int2*>(smemf + 2 * TILE);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
   const long n = (long)blockIdx.x * kPts1 + wave * 16 + c;
   const bool valid = n < N;
-  const float* xrow = X + (size_t)(valid ? n : 0) * d;
 
   float xq[Q];
   load_quarter32<Q, VEC>(X, n, N, d, g * Q, xq);
+  float xmax2 = 0.f;   // max_j x_j^2 of the point
+#pragma unroll
+  for (int j = 0; j < Q; j++) xmax2 = fmaxf(xmax2, xq[j] * xq[j]);
+  xmax2 = fmaxf(xmax2, __shfl_xor(xmax2, 16, 64));
+  xmax2 = fmaxf(xmax2, __shfl_xor(xmax2, 32, 64));
 
   const int ntiles = Kp / (16 * kSub1);
   f32x4 pre[PER];   // clang vector type, so the staging array stays in registers
@@ -143,29 +157,70 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   __syncthreads();
 
   float Mrun = -FLT_MAX;                  // max lower bound seen so far (all lane groups)
-  int pk[kPend];                          // pending window pairs: component (-1 = free)
-  float ph[kPend];                        // ... and its upper bound
-#pragma unroll
-  for (int i = 0; i < kPend; i++) {
-    pk[i] = -1;
-    ph[i] = -INFINITY;
-  }
+  int npend = 0;                          // entries in this lane's pending list
   double eM = -INFINITY, eS = 0.0;        // exact online log-sum-exp (base 2)
-  double s0v = -INFINITY, s1v = -INFINITY;  // two largest exact pairs (slots)
-  int s0k = -1, s1k = -1;
-  // exact evaluation of pair (n, k) folded into the sums and the slots
-#define FGMM_X1_TAKE(kk_)                                                             \
+  double sv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // largest exact pairs (slots)
+  int sk4[4] = {-1, -1, -1, -1};
+  // Evaluates the pending pairs still inside the window and empties the
+  // lists.  Wavefront-uniform: the four lanes of point c take turns as the
+  // source lane group gs; each computes its quarter of the fp64 distance of
+  // the source's i-th pair, two shuffles complete it, the source lane folds
+  // the exact value into its sums and slots.
+#define FGMM_X1_FLUSH(thr_)                                                           \
   {                                                                                   \
-    const int k_ = (kk_);                                                             \
-    const double v_ = exact_ll2(xrow, d, V, Kp, DP, b64, k_);                         \
-    const double mn_ = fmax(eM, v_);                                                  \
-    eS = eS * (double)exp2f((float)(eM - mn_)) + (double)exp2f((float)(v_ - mn_));    \
-    eM = mn_;                                                                         \
-    if (v_ > s0v) {                                                                   \
-      s1v = s0v; s1k = s0k; s0v = v_; s0k = k_;                                        \
-    } else if (v_ > s1v) {                                                            \
-      s1v = v_; s1k = k_;                                                              \
+    const float th_ = (thr_);                                                         \
+    int live_ = 0;                                                                    \
+    for (int i_ = 0; i_ < npend; i_++) {                                              \
+      const int2 e_ = plist[i_ * kThr1 + tid];                                        \
+      if (__int_as_float(e_.y) >= th_) {                                              \
+        plist[live_ * kThr1 + tid] = e_;                                              \
+        live_++;                                                                      \
+      }                                                                               \
     }                                                                                 \
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");                            \
+    __builtin_amdgcn_wave_barrier();                                                  \
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");                            \
+    int rounds_ = live_;                                                              \
+    _Pragma("unroll") for (int o_ = 32; o_ >= 1; o_ >>= 1)                            \
+        rounds_ = max(rounds_, __shfl_xor(rounds_, o_, 64));                          \
+    for (int i_ = 0; i_ < rounds_; i_++) {                                            \
+      _Pragma("unroll") for (int gs_ = 0; gs_ < 4; gs_++) {                           \
+        const int src_ = gs_ * 16 + c;                                                \
+        const bool go_ = i_ < __shfl(live_, src_, 64);                                \
+        if (__ballot(go_) != 0ull) {                                                  \
+          int k_ = 0;                                                                 \
+          double q_ = 0.0;                                                            \
+          if (go_) {                                                                  \
+            k_ = plist[i_ * kThr1 + wave * 64 + src_].x;                              \
+            const double2* cf_ =                                                      \
+                reinterpret_cast<const double2*>(V2) + (size_t)k_ * DP + g * Q;       \
+            _Pragma("unroll") for (int j_ = 0; j_ < Q; j_++) {                        \
+              const double2 sm_ = cf_[j_];                                            \
+              const double t_ = fma((double)xq[j_], sm_.x, -sm_.y);                   \
+              q_ = fma(t_, t_, q_);                                                   \
+            }                                                                         \
+          }                                                                           \
+          q_ += __shfl_xor(q_, 16, 64);                                               \
+          q_ += __shfl_xor(q_, 32, 64);                                               \
+          if (go_ && g == gs_) {                                                      \
+            const double v_ = b64[k_] - q_;                                           \
+            const double mn_ = fmax(eM, v_);                                          \
+            eS = eS * (double)exp2f((float)(eM - mn_)) + (double)exp2f((float)(v_ - mn_)); \
+            eM = mn_;                                                                 \
+            double cv_ = v_;                                                          \
+            int ck_ = k_;                                                             \
+            _Pragma("unroll") for (int q4_ = 0; q4_ < 4; q4_++) {                     \
+              if (cv_ > sv[q4_]) {                                                    \
+                const double tv_ = sv[q4_];                                           \
+                const int tk_ = sk4[q4_];                                             \
+                sv[q4_] = cv_; sk4[q4_] = ck_; cv_ = tv_; ck_ = tk_;                  \
+              }                                                                       \
+            }                                                                         \
+          }                                                                           \
+        }                                                                             \
+      }                                                                               \
+    }                                                                                 \
+    npend = 0;                                                                        \
   }
 
   for (int t = 0; t < ntiles; t++) {
@@ -207,20 +262,18 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
     lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
     Mrun = fmaxf(Mrun, lmax);
     const float thr = Mrun - kWin;
+    unsigned cm = 0;
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int kk = t * 16 * kSub1 + (u >> 2) * 16 + 4 * g + (u & 3);
-      bool placed = !(valid && hi[u] >= thr);
+    for (int u = 0; u < 8; u++) cm |= (valid && hi[u] >= thr) ? (1u << u) : 0u;
+    if (__ballot(cm != 0) != 0ull) {
+      if (__ballot(npend + __popc(cm) > kPendL) != 0ull) FGMM_X1_FLUSH(thr)
 #pragma unroll
-      for (int i = 0; i < kPend; i++) {
-        if (!placed && (pk[i] < 0 || ph[i] < thr)) {
-          pk[i] = kk;
-          ph[i] = hi[u];
-          placed = true;
+      for (int u = 0; u < 8; u++) {
+        if (cm & (1u << u)) {
+          const int kk = t * 16 * kSub1 + (u >> 2) * 16 + 4 * g + (u & 3);
+          plist[npend * kThr1 + tid] = make_int2(kk, __float_as_int(hi[u]));
+          npend++;
         }
-      }
-      if (__ballot(!placed) != 0ull) {
-        if (!placed) FGMM_X1_TAKE(kk)
       }
     }
     if (t + 1 < ntiles) FGMM_X1_LSTORE(buf ^ 1)
@@ -228,17 +281,8 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   }
 #undef FGMM_X1_GLOAD
 #undef FGMM_X1_LSTORE
-  {
-    const float thr = Mrun - kWin;
-#pragma unroll
-    for (int i = 0; i < kPend; i++) {
-      const bool go = pk[i] >= 0 && ph[i] >= thr;
-      if (__ballot(go) != 0ull) {
-        if (go) FGMM_X1_TAKE(pk[i])
-      }
-    }
-  }
-#undef FGMM_X1_TAKE
+  FGMM_X1_FLUSH(Mrun - kWin)
+#undef FGMM_X1_FLUSH
 
   // merge the exact sums of the four lane groups of each point
 #pragma unroll
@@ -254,15 +298,17 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   const double l2 = eM + log2(eS);
   const double lnat = l2 * kLn2;
   if (valid) {
-    const size_t base = (size_t)n * kSlots + 2 * g;
-    ck[base] = s0k >= 0 ? (unsigned short)s0k : kNoSlot;
-    ck[base + 1] = s1k >= 0 ? (unsigned short)s1k : kNoSlot;
-    cg[base] = s0k >= 0 ? exp2f((float)(s0v - l2)) : 0.f;
-    cg[base + 1] = s1k >= 0 ? exp2f((float)(s1v - l2)) : 0.f;
+    const size_t base = (size_t)n * kSlots + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      ck[base + q] = sk4[q] >= 0 ? (unsigned short)sk4[q] : kNoSlot;
+      cg[base + q] = sk4[q] >= 0 ? exp2f((float)(sv[q] - l2)) : 0.f;
+    }
     if (g == 0) {
       ln2[n] = l2;
       if (ln_out != nullptr) ln_out[n] = (float)lnat;
       m32[n] = Mrun;
+      xm[n] = xmax2;
     }
   }
   double contrib = (valid && g == 0) ? lnat : 0.0;
@@ -279,28 +325,39 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
 
 // ---------------------------------------------------------------------------
 // Pass 2.  Workgroup = 4 wavefronts x 16 components (fp32 coefficients in
-// registers), 64-point tiles of X, ln2, window anchors and slots
+// registers), 64-point tiles of X, per-point values and slots
 // double-buffered in LDS, XCD-aware workgroup mapping as the fp64 variant.
+// Per point the tile holds (ln2 as fp32, window threshold, max x^2, max |x|)
+// as one float4 and the exact ln2.  The slots of a tile that fall in this
+// workgroup's 64 components are scattered into a dense table gt[point]
+// [component] (-1 = no slot), double-buffered like the tile; thread t < 64
+// owns point row t, clearing the previous tile's entries of the buffer
+// before scattering the next tile's, so a window pair finds its exact
+// responsibility with one LDS read and the subtile loop has no branch.  A
+// window pair without a slot contributes nothing there and is added after
+// the tile with its exact responsibility (same statistics products).
 // ---------------------------------------------------------------------------
 template <int DP, bool VEC>
-__global__ __launch_bounds__(256) void pass2_x32_kernel(
+__global__ __launch_bounds__(kThr2) void pass2_x32_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const float* __restrict__ P32,
     const float* __restrict__ bias32, const float* __restrict__ Z32,
-    const double* __restrict__ V, const double* __restrict__ b64,
+    const double* __restrict__ V2, const double* __restrict__ b64,
     const double* __restrict__ ln2, const float* __restrict__ m32,
-    const unsigned short* __restrict__ ck, const float* __restrict__ cg,
-    double* __restrict__ part, long chunk, int nchunks, int kblocks, int stat_w) {
+    const float* __restrict__ xm, const unsigned short* __restrict__ ck,
+    const float* __restrict__ cg, double* __restrict__ part, long chunk, int nchunks,
+    int kblocks, int stat_w) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int XS = DP + 4;   // LDS row stride in floats
   constexpr int NFT = DP / 16;
-  constexpr int V4 = kTile2 * (DP / 4) / 256;
-  constexpr int CS = kTile2 * kSlots / 256;   // slots per thread per tile
+  constexpr int XV = kTile2 * (DP / 4);            // float4 per X tile
+  constexpr int V4 = (XV + kThr2 - 1) / kThr2;
   constexpr float Wslope = (float)(2.0 * x32_err_c(DP));
+  constexpr int GS = 16 * kW2 + 4;   // row stride of the slot table
   __shared__ float xs[2][kTile2 * XS];
+  __shared__ float4 pt[2][kTile2];
   __shared__ double ls[2][kTile2];
-  __shared__ float mt[2][kTile2];
-  __shared__ unsigned short sk[2][kTile2 * kSlots];
-  __shared__ float sg[2][kTile2 * kSlots];
+  __shared__ uint4 sk[2][kTile2][2];  // slot components of each point (16 x u16)
+  __shared__ float gt[2][kTile2 * GS];
 
   const int w = blockIdx.x;
   const int xcd = w & 7, local = w >> 3;
@@ -335,21 +392,23 @@ __global__ __launch_bounds__(256) void pass2_x32_kernel(
     accS[f] = f32x4{0.f, 0.f, 0.f, 0.f};
     accQ[f] = f64x4{0.0, 0.0, 0.0, 0.0};
   }
-  double nk = 0.0, ebound = 0.0;
+  double nk = 0.0;
+  float ebS = 0.f, esS = 0.f, eqS = 0.f;   // error bounds of the fp32 responsibilities
 
   float4 pre[V4];
-  unsigned short preK[CS];
-  float preG[CS];
+  const uint4 noslot = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+  uint4 preK[2] = {noslot, noslot};
+  float4 preG[4];
   double preL = 0.0;
-  float preM = 0.f;
+  float preM = 0.f, preX = 0.f;
   auto gload = [&](long t0) {
 #pragma unroll
     for (int i = 0; i < V4; i++) {
-      const int idx = tid + i * 256;
+      const int idx = tid + i * kThr2;
       const int row = idx / (DP / 4), j = 4 * (idx - row * (DP / 4));
       const long nn = t0 + row;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (nn < p1) {
+      if ((XV % kThr2 == 0 || idx < XV) && nn < p1) {
         const float* src = X + (size_t)nn * d + j;
         if (VEC) {
           if (j < d) v = *reinterpret_cast<const float4*>(src);
@@ -362,35 +421,62 @@ __global__ __launch_bounds__(256) void pass2_x32_kernel(
       }
       pre[i] = v;
     }
-#pragma unroll
-    for (int i = 0; i < CS; i++) {
-      const int idx = tid + i * 256;
-      const long nn = t0 + idx / kSlots;
-      const bool in = nn < p1;
-      preK[i] = in ? ck[(size_t)t0 * kSlots + idx] : kNoSlot;
-      preG[i] = in ? cg[(size_t)t0 * kSlots + idx] : 0.f;
-    }
     if (tid < kTile2) {
-      const bool in = t0 + tid < p1;
-      preL = in ? ln2[t0 + tid] : INFINITY;   // gamma = 0 past the chunk
-      preM = in ? m32[t0 + tid] : INFINITY;   // and no window there
+      const long nn = t0 + tid;
+      const bool in = nn < p1;
+      preL = in ? ln2[nn] : INFINITY;   // gamma = 0 past the chunk
+      preM = in ? m32[nn] : INFINITY;   // and no window there
+      preX = in ? xm[nn] : 0.f;
+      if (in) {
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+          preK[q] = reinterpret_cast<const uint4*>(ck + (size_t)nn * kSlots)[q];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          preG[q] = reinterpret_cast<const float4*>(cg + (size_t)nn * kSlots)[q];
+      } else {
+        preK[0] = preK[1] = noslot;
+      }
+    }
+  };
+  const int kbase = kb * 16 * kW2;
+  // point row tid of table buffer buf: clear the entries of the slots held
+  // in sk[buf][tid], then (if set) record and scatter the new slots
+  auto table_row = [&](int buf, bool set) {
+    const uint4 o0 = sk[buf][tid][0], o1 = sk[buf][tid][1];
+    const unsigned ow[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+    for (int i = 0; i < kSlots; i++) {
+      const int kl = (int)((ow[i >> 1] >> (16 * (i & 1))) & 0xFFFFu) - kbase;
+      if (kl >= 0 && kl < 16 * kW2) gt[buf][tid * GS + kl] = -1.f;
+    }
+    if (set) {
+      sk[buf][tid][0] = preK[0];
+      sk[buf][tid][1] = preK[1];
+      const unsigned nw[8] = {preK[0].x, preK[0].y, preK[0].z, preK[0].w,
+                              preK[1].x, preK[1].y, preK[1].z, preK[1].w};
+      const float gv[16] = {preG[0].x, preG[0].y, preG[0].z, preG[0].w,
+                            preG[1].x, preG[1].y, preG[1].z, preG[1].w,
+                            preG[2].x, preG[2].y, preG[2].z, preG[2].w,
+                            preG[3].x, preG[3].y, preG[3].z, preG[3].w};
+#pragma unroll
+      for (int i = 0; i < kSlots; i++) {
+        const int kl = (int)((nw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu) - kbase;
+        if (kl >= 0 && kl < 16 * kW2) gt[buf][tid * GS + kl] = gv[i];
+      }
     }
   };
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < V4; i++) {
-      const int idx = tid + i * 256;
+      const int idx = tid + i * kThr2;
       const int row = idx / (DP / 4), j = 4 * (idx - row * (DP / 4));
-      *reinterpret_cast<float4*>(&xs[buf][row * XS + j]) = pre[i];
-    }
-#pragma unroll
-    for (int i = 0; i < CS; i++) {
-      sk[buf][tid + i * 256] = preK[i];
-      sg[buf][tid + i * 256] = preG[i];
+      if (XV % kThr2 == 0 || idx < XV) *reinterpret_cast<float4*>(&xs[buf][row * XS + j]) = pre[i];
     }
     if (tid < kTile2) {
       ls[buf][tid] = preL;
-      mt[buf][tid] = preM;
+      pt[buf][tid] = make_float4((float)preL, preM - kWin, preX, sqrtf(preX));
+      table_row(buf, true);
     }
   };
 
@@ -415,6 +501,13 @@ __global__ __launch_bounds__(256) void pass2_x32_kernel(
     accQ[f] = mfma64((double)gm[r], xd * xd, accQ[f]);
   };
 
+  for (int i = tid; i < 2 * kTile2 * GS; i += kThr2) (&gt[0][0])[i] = -1.f;
+  if (tid < kTile2) {   // no slots yet
+    sk[0][tid][0] = sk[0][tid][1] = noslot;
+    sk[1][tid][0] = sk[1][tid][1] = noslot;
+  }
+  __syncthreads();
+
   const long ntile = (p1 > p0) ? (p1 - p0 + kTile2 - 1) / kTile2 : 0;
   if (ntile > 0) {
     gload(p0);
@@ -430,49 +523,75 @@ __global__ __launch_bounds__(256) void pass2_x32_kernel(
       f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = f32x4{bk, bk, bk, bk};
 #pragma unroll
       for (int s4 = 0; s4 < Q / 4; s4++) gemm1_block(xt + c * XS + g * Q, s4, a0, a1);
+      float nkt = 0.f;
+      unsigned miss = 0;   // bit 4*sub + r: window pair without a slot
+      // responsibility of pair (sub, r) from GEMM1's accumulators (a0, a1)
+      auto gamma_pair = [&](int sub, int r, const f32x4& x0, const f32x4& x1, float& gr) {
+        const int pl = sub * 16 + 4 * g + r;
+        const float4 P = pt[buf][pl];
+        const float tab = gt[buf][pl * GS + wave * 16 + c];
+        const float ll = x0[r] + x1[r];
+        const float hi = ll + fmaf(Wslope, -x0[r], zk);
+        const float gam = exp2f(ll - P.x);
+        const bool win = hi >= P.y;
+        // bound of the true gamma: the pair's upper bound and the rounding of
+        // ln2 to fp32 (|ln2| 2^-24)
+        const float hb = fmaf(fabsf(P.x), 6.0e-8f, hi);
+        const float e = win ? 0.f : exp2f(hb - P.x) - gam;
+        ebS += e;
+        esS = fmaf(e, P.w, esS);
+        eqS = fmaf(e, P.z, eqS);
+        // window pair: the exact responsibility from the slot table (a
+        // missing slot contributes after the tile)
+        gr = win ? fmaxf(tab, 0.f) : gam;
+        miss |= (win && tab < 0.f) ? (1u << (4 * sub + r)) : 0u;
+      };
 #pragma unroll
       for (int sub = 0; sub < kTile2 / 16; sub++) {
+        // gamma(sub) interleaved with the distance product of subtile sub+1
+        // (independent), then the statistics products of subtile sub
         float gm[4];
+        f32x4 b0 = f32x4{0.f, 0.f, 0.f, 0.f}, b1 = f32x4{bk, bk, bk, bk};
+        const float* xr = xt + ((sub + 1) * 16 + c) * XS + g * Q;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int pl = sub * 16 + 4 * g + r;
-          const float ll = a0[r] + a1[r];
-          const float hi = ll + fmaf(Wslope, -a0[r], zk);
-          const double lnp = ls[buf][pl];
-          float gam;
-          if (hi >= mt[buf][pl] - kWin) {
-            // window pair: exact responsibility from the slots, else recomputed
-            gam = -1.f;
-#pragma unroll
-            for (int i = 0; i < kSlots; i++)
-              if (sk[buf][pl * kSlots + i] == (unsigned short)kmine) gam = sg[buf][pl * kSlots + i];
-            if (gam < 0.f)
-              gam = exp2f((float)(exact_ll2(X + (size_t)(t0 + pl) * d, d, V, Kp, DP, b64,
-                                            kmine) - lnp));
-          } else {
-            gam = exp2f((float)((double)ll - lnp));
-            ebound += (double)(exp2f((float)((double)hi - lnp)) - gam);
-          }
-          gm[r] = gam;
-          nk += (double)gam;
+        for (int s4 = 0; s4 < Q / 4; s4++) {
+          if (sub + 1 < kTile2 / 16) gemm1_block(xr, s4, b0, b1);
+          if (s4 < 4) gamma_pair(sub, s4, a0, a1, gm[s4]);
         }
+#pragma unroll
+        for (int r = Q / 4; r < 4; r++) gamma_pair(sub, r, a0, a1, gm[r]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) nkt += gm[r];
         const float* xsub = xt + sub * 16 * XS;
-        if (sub + 1 < kTile2 / 16) {
-          const float* xr = xt + ((sub + 1) * 16 + c) * XS + g * Q;
-          f32x4 b0 = f32x4{0.f, 0.f, 0.f, 0.f}, b1 = f32x4{bk, bk, bk, bk};
 #pragma unroll
-          for (int s4 = 0; s4 < Q / 4; s4++) {
-            gemm1_block(xr, s4, b0, b1);
+        for (int p = 0; p < 4 * NFT; p++) gemm2_pair(xsub, gm, p);
+        a0 = b0;
+        a1 = b1;
+      }
+      if (__ballot(miss != 0) != 0ull) {
+        // window pairs without a slot: exact responsibility, same products
 #pragma unroll
-            for (int u = 0; u < 4; u++) gemm2_pair(xsub, gm, 4 * s4 + u);
+        for (int sub = 0; sub < kTile2 / 16; sub++) {
+          const unsigned sm = (miss >> (4 * sub)) & 15u;
+          if (__ballot(sm != 0) != 0ull) {
+            float gm[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              gm[r] = 0.f;
+              if (sm & (1u << r)) {
+                const int pl = sub * 16 + 4 * g + r;
+                gm[r] = exp2f((float)(exact_ll2(X + (size_t)(t0 + pl) * d, d, V2, DP, b64,
+                                                kmine) - ls[buf][pl]));
+              }
+              nkt += gm[r];
+            }
+            const float* xsub = xt + sub * 16 * XS;
+#pragma unroll
+            for (int p = 0; p < 4 * NFT; p++) gemm2_pair(xsub, gm, p);
           }
-          a0 = b0;
-          a1 = b1;
-        } else {
-#pragma unroll
-          for (int p = 0; p < 4 * NFT; p++) gemm2_pair(xsub, gm, p);
         }
       }
+      nk += (double)nkt;
     }
     if (it + 1 < ntile) lstore(buf ^ 1);
     __syncthreads();
@@ -488,23 +607,97 @@ __global__ __launch_bounds__(256) void pass2_x32_kernel(
       out[(size_t)(4 * r + g) * stat_w + DP + f * 16 + c] = accQ[f][r];
     }
   }
-  nk += __shfl_xor(nk, 16, 64);
-  nk += __shfl_xor(nk, 32, 64);
-  ebound += __shfl_xor(ebound, 16, 64);
-  ebound += __shfl_xor(ebound, 32, 64);
+  double e1 = (double)ebS, e2 = (double)esS, e3 = (double)eqS;
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    nk += __shfl_xor(nk, off, 64);
+    e1 += __shfl_xor(e1, off, 64);
+    e2 += __shfl_xor(e2, off, 64);
+    e3 += __shfl_xor(e3, off, 64);
+  }
   if (g == 0) {
-    out[(size_t)c * stat_w + 2 * DP] = nk;
-    out[(size_t)c * stat_w + 2 * DP + 1] = ebound;
+    double* o = out + (size_t)c * stat_w + 2 * DP;
+    o[0] = nk;
+    o[1] = e1;
+    o[2] = e2;
+    o[3] = e3;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exact statistics of the flagged components.  Block (chunk s, group q)
+// handles components k = q, q + G, ... with flag[k] set: 256 points at a time,
+// thread t evaluates the exact responsibility of point t (fp64 direct form,
+// fp64 exp2), then threads (j, half) accumulate gamma x_j and gamma x_j^2 over
+// their half of the points; the result overwrites the Pass-2 partial row
+// [s][k].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void x32_fix_kernel(
+    const float* __restrict__ X, long N, int d, int K, int Kp, int dp,
+    const double* __restrict__ V2, const double* __restrict__ b64,
+    const double* __restrict__ ln2, const int* __restrict__ flag,
+    double* __restrict__ part, long chunk, int stat_w) {
+  __shared__ double gsh[256];
+  __shared__ double hsa[128], hsb[128];
+  __shared__ double red[4];
+  const int s = blockIdx.x, G = gridDim.y;
+  const int tid = threadIdx.x, j = tid & 127, half = tid >> 7;
+  const long p0 = (long)s * chunk;
+  const long p1 = (p0 + chunk < N) ? p0 + chunk : N;
+  for (int k = blockIdx.y; k < K; k += G) {
+    if (flag[k] == 0) continue;
+    double sa = 0.0, sb = 0.0, sn = 0.0;
+    for (long base = p0; base < p1; base += 256) {
+      const long nn = base + tid;
+      double gam = 0.0;
+      if (nn < p1) gam = exp2(exact_ll2(X + (size_t)nn * d, d, V2, dp, b64, k) - ln2[nn]);
+      sn += gam;
+      __syncthreads();
+      gsh[tid] = gam;
+      __syncthreads();
+      const int cnt = (p1 - base < 256) ? (int)(p1 - base) : 256;
+      if (j < d) {
+        for (int i = half; i < cnt; i += 2) {
+          const double x = (double)X[(size_t)(base + i) * d + j];
+          sa = fma(gsh[i], x, sa);
+          sb = fma(gsh[i], x * x, sb);
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sn += __shfl_xor(sn, off, 64);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = sn;
+    if (half == 1) {
+      hsa[j] = sa;
+      hsb[j] = sb;
+    }
+    __syncthreads();
+    double* o = part + ((size_t)s * Kp + k) * stat_w;
+    if (half == 0 && j < d) {
+      o[j] = sa + hsa[j];
+      o[dp + j] = sb + hsb[j];
+    }
+    if (tid == 0) o[2 * dp] = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
   }
 }
 
 template <int DP, bool VEC>
 hipError_t x1_launch(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                      float* ln_out, double* lnsum, hipStream_t s) {
-  constexpr size_t lds = 2 * (size_t)kSub1 * (DP / 2) * 64 * sizeof(float);
+  constexpr size_t lds = 2 * (size_t)kSub1 * (DP / 2) * 64 * sizeof(float) +
+                         (size_t)kPendL * kThr1 * sizeof(int2);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)pass1_x32_kernel<DP, VEC>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
   hipLaunchKernelGGL((pass1_x32_kernel<DP, VEC>), dim3(g.p1_blocks), dim3(kThr1), lds, s, X,
                      g.N, g.d, g.Kp, w.P32, w.bias32, w.Z32, w.V, w.b64, ln2, ln_out, lnsum,
-                     w.m32, w.ck, w.cg);
+                     w.m32, w.xm, w.ck, w.cg);
   return hipGetLastError();
 }
 
@@ -513,11 +706,13 @@ hipError_t x2_launch(const Geom& g, const float* X, const X32Ws& w, const double
                      double* part, hipStream_t s) {
   const int padded = (g.p2_chunks + 7) / 8 * 8;
   hipLaunchKernelGGL((pass2_x32_kernel<DP, VEC>), dim3(g.p2_kblocks * padded),
-                     dim3(64 * kW2), 0, s, X, g.N, g.d, g.Kp, w.P32, w.bias32, w.Z32, w.V,
-                     w.b64, ln2, w.m32, w.ck, w.cg, part, g.p2_chunk, g.p2_chunks,
+                     dim3(kThr2), 0, s, X, g.N, g.d, g.Kp, w.P32, w.bias32, w.Z32, w.V,
+                     w.b64, ln2, w.m32, w.xm, w.ck, w.cg, part, g.p2_chunk, g.p2_chunks,
                      g.p2_kblocks, g.stat_w);
   return hipGetLastError();
 }
+
+constexpr int kFixGroups = 8;   // component groups per point chunk in x32_fix_kernel
 
 }  // namespace
 
@@ -539,10 +734,19 @@ hipError_t launch_pass1_x32(const Geom& g, const float* X, const X32Ws& w, doubl
   }
 }
 
+hipError_t launch_x32_fix(const Geom& g, const float* X, const X32Ws& w, const double* ln2,
+                          double* part, hipStream_t s) {
+  if (g.d > 128) return hipErrorInvalidValue;   // one thread per feature and half
+  hipLaunchKernelGGL(x32_fix_kernel, dim3(g.p2_chunks, kFixGroups), dim3(256), 0, s, X, g.N,
+                     g.d, g.K, g.Kp, g.dp, w.V, w.b64, ln2, w.flag, part, g.p2_chunk,
+                     g.stat_w);
+  return hipGetLastError();
+}
+
 hipError_t launch_pass2_x32(const Geom& g, const float* X, const X32Ws& w,
                             const double* ln2, double* part, hipStream_t s) {
-  // the partial row holds the error-bound column after sum gamma
-  if (g.stat_w < 2 * g.dp + 2) return hipErrorInvalidValue;
+  // the partial row holds the three error-bound columns after sum gamma
+  if (g.stat_w < 2 * g.dp + 4) return hipErrorInvalidValue;
   const bool v = x_is_vec(X, g.d);
   switch (g.dp) {
 #define FGMM_X2(D)                                               \
