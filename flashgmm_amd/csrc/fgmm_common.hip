@@ -230,7 +230,8 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
       const double m = fabs(a) / ncl, q = fabs(b) / ncl;
       const double dmu = (es + m * eb) / ncl;
       const double dvar = (eq + q * eb + 2.0 * m * (es + m * eb)) / ncl;
-      if (dmu > kX32Guard || dvar > kX32Guard || eb / ncl > kX32Guard) bad_sh = 1;
+      // written so that a NaN bound flags the component as well
+      if (!(dmu <= kX32Guard && dvar <= kX32Guard && eb / ncl <= kX32Guard)) bad_sh = 1;
     }
   }
   __syncthreads();

@@ -475,7 +475,9 @@ __global__ __launch_bounds__(kThr2) void pass2_x32_kernel(
     }
     if (tid < kTile2) {
       ls[buf][tid] = preL;
-      pt[buf][tid] = make_float4((float)preL, preM - kWin, preX, sqrtf(preX));
+      // past the chunk: a finite stand-in for +inf keeps every term of the
+      // pair's error bound finite (gamma and bound both 0)
+      pt[buf][tid] = make_float4(fminf((float)preL, 3.0e38f), preM - kWin, preX, sqrtf(preX));
       table_row(buf, true);
     }
   };

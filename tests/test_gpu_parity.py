@@ -260,3 +260,52 @@ def test_native_library_is_what_ran(cuda):
     from flashgmm_amd import _lib
     maps = open("/proc/self/maps").read()
     assert _lib.LIB_PATH in maps
+
+
+def test_x32_starved_component_takes_exact_path(cuda):
+    """A clone of a 16384-point component weighted 2^-41 below it: every
+    responsibility of the clone lies just outside the exact window, where x32
+    uses fp32 responsibilities, and their sum (7.5e-9) sits at the n_k clamp,
+    so the clone's mean and variance (~0.75 of the original's moments) carry
+    the fp32 rounding of its bias and distances undiluted.  Its error bounds
+    flag it and its statistics are recomputed exactly."""
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(3)
+    N, d = 20000, 64
+    centers = rng.uniform(-4, 4, (5, d))
+    labels = np.concatenate([np.zeros(16384, int), rng.integers(1, 4, N - 16384)])
+    X = (centers[labels] + rng.normal(0, 1, (N, d))).astype(np.float32)
+    mu = centers.astype(np.float32)
+    mu[4] = mu[0]
+    var = np.ones((5, d), np.float32)
+    lp = np.full(5, -np.log(5), np.float32)
+    lp[4] = lp[0] - 41 * np.log(2.0)
+    _, _, _, ln, (n_k, s_k, sq_k) = O.c_em_fused(X, mu, var, lp, with_stats=True)
+    ref = O.c_m_step_update(n_k, s_k, sq_k, N)
+    assert 1e-9 < n_k[4] < 1e-8, n_k[4]      # starved, at the clamp
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in ("x32", "mfma"):
+        print(f"[case] starved component variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
+        check_ln(out[3], ln, f"starved {variant}")
+        check_params(out[:3], ref, f"starved {variant}")
+
+
+def test_x32_crowded_window_overflows_slots(cuda):
+    """64 nearly identical components: every point has ~64 pairs inside the
+    exact window, far more than its 16 slots, so Pass 2 recomputes the
+    missing ones."""
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(7)
+    N, K, d = 4096, 64, 32
+    X = rng.normal(0, 1, (N, d)).astype(np.float32)
+    mu = (rng.normal(0, 0.02, (K, d))).astype(np.float32)
+    var = rng.uniform(0.9, 1.1, (K, d)).astype(np.float32)
+    lp = np.full(K, -np.log(K), np.float32)
+    ref = O.c_em_fused(X, mu, var, lp)
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in ("x32", "mfma"):
+        print(f"[case] crowded window variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
+        check_ln(out[3], ref[3], f"crowded {variant}")
+        check_params(out[:3], ref[:3], f"crowded {variant}")
