@@ -36,6 +36,10 @@ SIGNATURES = {
     "fgmm_standard_e_step": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _Z, _P], _I),
     "fgmm_standard_m_step_workspace_bytes": ([_L, _I, _I], _Z),
     "fgmm_standard_m_step": ([_P, _P, _L, _I, _I, _P, _P, _P, _P, _Z, _P], _I),
+    "fgmm_stream_workspace_bytes": ([_L, _I, _I, _I], _Z),
+    "fgmm_stream_begin": ([_P, _P, _P, _L, _I, _I, _I, _P, _Z, _P], _I),
+    "fgmm_stream_chunk": ([_P, _L, _L, _I, _I, _I, _P, _P, _Z, _P], _I),
+    "fgmm_stream_end": ([_L, _L, _I, _I, _I, _P, _P, _P, _P, _P, _Z, _P], _I),
     "fgmm_profile_enable": ([_I], _I),
     "fgmm_profile_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)], _I),
 }

@@ -294,6 +294,16 @@ static int validate_ws_bytes(void* ws, size_t bytes, size_t need) {
   return FGMM_OK;
 }
 
+// Streaming workspace: [acc fp64 Kp x stat_w | acc_ln fp64 | pad] then the
+// workspace of one chunk of up to chunk_rows points.  The accumulator sits at
+// a fixed offset, so every chunk size up to chunk_rows shares it (the chunk
+// regions only grow with the number of rows, and the coefficient regions of
+// a chunk do not depend on it).
+static size_t stream_acc_bytes(const Geom& g) {
+  return align256(sizeof(double) * ((size_t)g.Kp * g.stat_w + 1));
+}
+static int stream_variant(int variant) { return variant == kX32 ? kMfma : variant; }
+
 }  // namespace fgmm
 
 using namespace fgmm;
@@ -500,6 +510,106 @@ int fgmm_standard_m_step(const float* X, const float* gamma, long N, int K, int 
   return check_hip(launch_reduce(g, part, nullptr, nullptr, nullptr, nullptr, mu, var, log_pi,
                                  nullptr, nullptr, nullptr, s, /*standard=*/1),
                    "standard M-step");
+}
+
+// Workspace bound of one chunk of any size up to chunk_rows: the partial
+// block count of make_geom is not monotone in N (chunks round up to 64
+// points), so it is bounded by min(tiles, max(ceil(512/kblocks),
+// ceil(N/16384))) at N = chunk_rows; every other region grows with N.
+static size_t stream_chunk_bytes(long chunk_rows, int K, int d, int variant) {
+  Geom g = make_geom(chunk_rows, K, d, variant);
+  const long tiles = (chunk_rows + 63) / 64;
+  long smax = (512 + g.p2_kblocks - 1) / g.p2_kblocks;
+  if (smax < (chunk_rows + 16383) / 16384) smax = (chunk_rows + 16383) / 16384;
+  if (smax > tiles) smax = tiles;
+  if (smax < g.p2_chunks) smax = g.p2_chunks;
+  g.p2_chunks = (int)smax;
+  return make_layout(g).total;
+}
+
+size_t fgmm_stream_workspace_bytes(long chunk_rows, int K, int d, int variant) {
+  variant = stream_variant(variant);
+  if (validate_shape(chunk_rows, K, d, variant) != FGMM_OK) return 0;
+  Geom g = make_geom(chunk_rows, K, d, variant);
+  return stream_acc_bytes(g) + stream_chunk_bytes(chunk_rows, K, d, variant);
+}
+
+// Chunk geometry and workspace views of a streaming call.
+static int stream_setup(long rows, long chunk_rows, int K, int d, int variant, void* ws,
+                        size_t ws_bytes, Geom& g, Ws& w, double*& acc, double*& acc_ln) {
+  int rc = validate_shape(chunk_rows, K, d, variant);
+  if (rc) return rc;
+  if (rows < 1 || rows > chunk_rows)
+    return fail(FGMM_EINVAL, "chunk rows must be in [1, %ld] (got %ld)", chunk_rows, rows);
+  Geom gc = make_geom(chunk_rows, K, d, variant);
+  const size_t ab = stream_acc_bytes(gc);
+  if ((rc = validate_ws_bytes(ws, ws_bytes, ab + stream_chunk_bytes(chunk_rows, K, d, variant))))
+    return rc;
+  g = make_geom(rows, K, d, variant);
+  WsLayout L = make_layout(g);
+  if (ab + L.total > ws_bytes)   // covered by the bound above; checked regardless
+    return fail(FGMM_EWORKSPACE, "internal: chunk of %ld rows exceeds the stream workspace", rows);
+  w = carve(g, static_cast<char*>(ws) + ab, L);
+  acc = static_cast<double*>(ws);
+  acc_ln = acc + (size_t)gc.Kp * gc.stat_w;
+  return FGMM_OK;
+}
+
+int fgmm_stream_begin(const float* mu, const float* var, const float* log_pi, long chunk_rows,
+                      int K, int d, int variant, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  variant = stream_variant(variant);
+  FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  Geom g;
+  Ws w;
+  double *acc, *acc_ln;
+  int rc = stream_setup(chunk_rows, chunk_rows, K, d, variant, ws, ws_bytes, g, w, acc, acc_ln);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((rc = check_hip(launch_zero_f64(acc, (size_t)g.Kp * g.stat_w + 1, s), "stream reset")))
+    return rc;
+  return run_precompute(g, mu, var, log_pi, w, s);
+}
+
+int fgmm_stream_chunk(const float* X, long rows, long chunk_rows, int K, int d, int variant,
+                      float* log_normalizer, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  variant = stream_variant(variant);
+  FGMM_REQUIRE(X);
+  Geom g;
+  Ws w;
+  double *acc, *acc_ln;
+  int rc = stream_setup(rows, chunk_rows, K, d, variant, ws, ws_bytes, g, w, acc, acc_ln);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
+  if ((rc = run_pass2(g, X, w, s))) return rc;
+  Timed t(3, s);
+  return check_hip(launch_accumulate(g, w.part, w.lnsum, acc, acc_ln, s), "stream accumulate");
+}
+
+int fgmm_stream_end(long N, long chunk_rows, int K, int d, int variant, float* new_mu,
+                    float* new_var, float* new_log_pi, double* ll_mean, void* ws,
+                    size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  variant = stream_variant(variant);
+  FGMM_REQUIRE(new_mu); FGMM_REQUIRE(new_var); FGMM_REQUIRE(new_log_pi);
+  if (N < 1) return fail(FGMM_EINVAL, "N must be >= 1 (got %ld)", N);
+  Geom gc;
+  Ws w;
+  double *acc, *acc_ln;
+  int rc = stream_setup(chunk_rows, chunk_rows, K, d, variant, ws, ws_bytes, gc, w, acc, acc_ln);
+  if (rc) return rc;
+  // the accumulator is one partial block over all N points
+  Geom g = gc;
+  g.N = N;
+  g.p2_chunks = 1;
+  g.p1_blocks = 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Timed t(3, s);
+  return check_hip(launch_reduce(g, acc, acc_ln, nullptr, nullptr, nullptr, new_mu, new_var,
+                                 new_log_pi, nullptr, nullptr, ll_mean, s),
+                   "stream M-step");
 }
 
 int fgmm_profile_enable(int enable) {

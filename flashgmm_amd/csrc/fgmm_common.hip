@@ -289,6 +289,53 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
 }
 
 // ---------------------------------------------------------------------------
+// Streaming accumulation (one chunk of points at a time): the chunk's Pass-2
+// partials are folded into a running fp64 accumulator laid out like one
+// partial row block, [Kp][stat_w], so the M-step can reduce it as S = 1.
+// One block per (component, 128-column slice); fixed summation order.
+// ---------------------------------------------------------------------------
+__global__ void accumulate_kernel(int S, int Kp, int width, int stat_w,
+                                  const double* __restrict__ part,
+                                  const double* __restrict__ lnsum, int n_lnsum,
+                                  double* __restrict__ acc, double* __restrict__ acc_ln) {
+  __shared__ double red[16];
+  const int k = blockIdx.x;
+  const int c = blockIdx.y * blockDim.x + threadIdx.x;
+  if (c < width) {
+    double t = 0.0;
+    for (int s = 0; s < S; s++) t += part[((size_t)s * Kp + k) * stat_w + c];
+    acc[(size_t)k * stat_w + c] += t;
+  }
+  if (k == 0 && blockIdx.y == 0) {
+    double t = 0.0;
+    for (int i = threadIdx.x; i < n_lnsum; i += blockDim.x) t += lnsum[i];
+    t = block_sum_f64(t, red);
+    if (threadIdx.x == 0) acc_ln[0] += t;
+  }
+}
+
+hipError_t launch_accumulate(const Geom& g, const double* part, const double* lnsum,
+                             double* acc, double* acc_ln, hipStream_t s) {
+  const int width = 2 * g.dp + 1;
+  const dim3 grid(g.Kp, (width + 127) / 128);
+  hipLaunchKernelGGL(accumulate_kernel, grid, dim3(128), 0, s, g.p2_chunks, g.Kp, width,
+                     g.stat_w, part, lnsum, g.p1_blocks, acc, acc_ln);
+  return hipGetLastError();
+}
+
+// Fill kernel (used instead of a memset so the sequence stays capturable).
+__global__ void zero_f64_kernel(double* __restrict__ p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0;
+}
+
+hipError_t launch_zero_f64(double* p, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_f64_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Standalone M-step on fp32 statistics (flash_gmm_cuda.cu:298-322 semantics,
 // evaluated in fp64 and rounded once).
 // ---------------------------------------------------------------------------

@@ -150,6 +150,11 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s,
                          int standard = 0, int stage = kReduceAll, int* flag = nullptr);
+// Streaming: acc[k][c] += sum_s part[s][k][c] for c < 2dp+1 (fixed order over
+// s), acc_ln[0] += sum of the Pass-1 workgroup sums.
+hipError_t launch_accumulate(const Geom& g, const double* part, const double* lnsum,
+                             double* acc, double* acc_ln, hipStream_t s);
+hipError_t launch_zero_f64(double* p, size_t n, hipStream_t s);
 // Exact partials [chunk][k][*] of the flagged components (x32).
 hipError_t launch_x32_fix(const Geom& g, const float* X, const X32Ws& w, const double* ln2,
                           double* part, hipStream_t s);

@@ -168,6 +168,37 @@ int fgmm_standard_m_step(const float* X, const float* gamma, long N, int K, int 
                          void* stream);
 
 /*
+ * Streaming EM iteration for X that does not fit in device memory (or is
+ * produced chunk by chunk): the sufficient statistics of Pass 2 are additive
+ * over point chunks, so the caller feeds chunks of at most chunk_rows points
+ * (device pointers; e.g. copied from pinned host memory while the previous
+ * chunk computes) between a begin and an end call:
+ *   fgmm_stream_begin  precompute the coefficients of (mu, var, log_pi) and
+ *                      clear the fp64 accumulators;
+ *   fgmm_stream_chunk  Pass 1 + Pass 2 on `rows` points; log_normalizer
+ *                      (nullable, [rows]) receives their log p(x); statistics
+ *                      and sum(ln) are added to the accumulators in a fixed
+ *                      order (results do not depend on timing);
+ *   fgmm_stream_end    M-step over all N points (native clamps); ll_mean
+ *                      (nullable, device double) = mean log-normalizer.
+ * All calls of one iteration use the same workspace (of
+ * fgmm_stream_workspace_bytes(chunk_rows, ...)), chunk_rows and variant, in
+ * stream order.  FGMM_VARIANT_X32 runs as MFMA here.
+ * Replaces the streaming iteration of StreamingFlashGMM / StreamingFlashGMMAsync
+ * .em_step (flash_gmm/flash_gmm_v9.py:145-326), which makes one pass over
+ * the chunks per stage; here each chunk is read once per iteration.
+ */
+size_t fgmm_stream_workspace_bytes(long chunk_rows, int K, int d, int variant);
+int fgmm_stream_begin(const float* mu, const float* var, const float* log_pi,
+                      long chunk_rows, int K, int d, int variant, void* ws, size_t ws_bytes,
+                      void* stream);
+int fgmm_stream_chunk(const float* X, long rows, long chunk_rows, int K, int d, int variant,
+                      float* log_normalizer, void* ws, size_t ws_bytes, void* stream);
+int fgmm_stream_end(long N, long chunk_rows, int K, int d, int variant, float* new_mu,
+                    float* new_var, float* new_log_pi, double* ll_mean, void* ws,
+                    size_t ws_bytes, void* stream);
+
+/*
  * Kernel timing with HIP events recorded on the launch stream around every
  * kernel this library queues, while enabled.  fgmm_profile_read waits for
  * the recorded events, then fills ms_total[i] and launches[i] for

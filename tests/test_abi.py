@@ -151,3 +151,31 @@ def test_python_errors_mirror_reference():
     with pytest.raises(RuntimeError, match="unknown variant"):
         from flashgmm_amd import _lib
         _lib.variant_code("fast")
+
+
+def test_stream_argument_errors(lib):
+    ws = 1 << 30
+    b = lib.fgmm_stream_workspace_bytes(1000, 8, 16, 0)
+    assert b > 0 and b % 256 == 0
+    assert lib.fgmm_stream_workspace_bytes(1000, 8, 16, 3) == lib.fgmm_stream_workspace_bytes(1000, 8, 16, 2)
+    assert lib.fgmm_stream_workspace_bytes(0, 8, 16, 0) == 0
+    # a chunk larger than the chunk size the workspace was made for
+    assert lib.fgmm_stream_chunk(0x1000, 1001, 1000, 8, 16, 0, None, 0x1000, ws, None) == 1
+    assert b"chunk rows" in lib.fgmm_last_error()
+    assert lib.fgmm_stream_chunk(None, 10, 1000, 8, 16, 0, None, 0x1000, ws, None) == 1
+    assert lib.fgmm_stream_chunk(0x1000, 10, 1000, 8, 16, 0, None, 0x1000, 64, None) == 2
+    assert lib.fgmm_stream_end(0, 1000, 8, 16, 0, 0x1000, 0x1000, 0x1000, None, 0x1000, ws, None) == 1
+    assert lib.fgmm_stream_begin(None, 0x1000, 0x1000, 1000, 8, 16, 0, 0x1000, ws, None) == 1
+
+
+def test_streaming_python_errors():
+    import torch
+    from flashgmm_amd import streaming
+    X = torch.zeros(10, 4)
+    mu, var, lp = torch.zeros(2, 4), torch.ones(2, 4), torch.zeros(2)
+    with pytest.raises(RuntimeError, match="X must be float32"):
+        streaming.StreamingFlashGMM(4).em_step(X.double(), mu, var, lp)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        streaming.StreamingFlashGMMAsync(4).em_step(X, mu, var, lp)
+    with pytest.raises(RuntimeError, match="chunk_size"):
+        streaming.StreamingFlashGMM(0)
