@@ -38,8 +38,12 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // a 16x16 tile (K is padded to 32) and hold the 16-component coefficient
 // fragment in registers up to d = 128; below or above that the vector-ALU
 // kernels run.
+// From K >= 256 the x32 Pass 1 (fp32 candidates, exact log-normalizer) beats
+// the fp64 one by 20-27 % at d = 64 and 128 (measured; at K = 128 its
+// candidate work outweighs the saving), so auto pairs it with the fp64 Pass 2.
 static int resolve_variant(int K, int d, int variant) {
-  if (variant == kValu || variant == kMfma || variant == kX32) return variant;
+  if (variant >= kValu && variant <= kMixed) return variant;
+  if (d <= 128 && K >= 256) return kMixed;
   if (d <= 128 && K >= 16) return kMfma;
   return kValu;
 }
@@ -50,7 +54,7 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.K = K;
   g.d = d;
   g.variant = resolve_variant(K, d, variant);
-  if (g.variant == kMfma || g.variant == kX32) {
+  if (g.variant == kMfma || g.variant == kX32 || g.variant == kMixed) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
     g.p1_blocks = (int)((N + 127) / 128);
@@ -85,12 +89,14 @@ WsLayout make_layout(const Geom& g) {
   WsLayout L;
   size_t off = 0;
   const bool x32 = g.variant == kX32;
+  const bool xset = x32 || g.variant == kMixed;        // holds the x32 coefficient set
+  const size_t kd2 = 2 * (size_t)g.Kp * g.dp;
   L.params = off;
-  off = align256(off + sizeof(double) * 2 * (size_t)g.Kp * g.dp +
-                 (x32 ? sizeof(float) * 2 * (size_t)g.Kp * g.dp : 0));
+  off = align256(off + sizeof(double) * kd2 * (g.variant == kMixed ? 2 : 1) +
+                 (xset ? sizeof(float) * kd2 : 0));
   L.bias = off;
-  off = align256(off + sizeof(double) * (size_t)g.Kp +
-                 (x32 ? (sizeof(float) + sizeof(int)) * (size_t)g.Kp : 0));
+  off = align256(off + sizeof(double) * (size_t)g.Kp * (g.variant == kMixed ? 2 : 1) +
+                 (xset ? 2 * sizeof(float) * (size_t)g.Kp : 0));
   L.ln2 = off;
   off = align256(off + sizeof(double) * (size_t)g.N);
   L.lnsum = off;
@@ -157,8 +163,10 @@ static int validate_shape(long N, int K, int d, int variant) {
   if (K > 65536) return fail(FGMM_EINVAL, "K must be <= 65536 (got %d)", K);
   if (d < 1 || d > kMaxD)
     return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
-  if (variant < 0 || variant > 3)
+  if (variant < 0 || variant > kMixed)
     return fail(FGMM_EINVAL, "unknown variant %d", variant);
+  if (variant == kMixed && d > 128)
+    return fail(FGMM_EINVAL, "the mixed variant supports d <= 128 (got %d)", d);
   if (variant == kMfma && d > 128)
     return fail(FGMM_EINVAL, "the MFMA variant supports d <= 128 (got %d)", d);
   if (variant == kX32 && (d > 128 || K > 32768))
@@ -195,6 +203,14 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
   Ws w{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
        reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
        reinterpret_cast<double*>(b + L.part), X32Ws{}, true};
+  if (g.variant == kMixed) {   // x32 set behind the fp64 one; no slots
+    const size_t kd2 = 2 * (size_t)g.Kp * g.dp;
+    w.x.V = w.params + kd2;
+    w.x.P32 = reinterpret_cast<const float*>(w.params + 2 * kd2);
+    w.x.b64 = w.bias + g.Kp;
+    w.x.bias32 = reinterpret_cast<const float*>(w.bias + 2 * g.Kp);
+    w.x.Z32 = w.x.bias32 + g.Kp;
+  }
   if (g.variant == kX32) {
     const size_t N = (size_t)g.N;
     w.x.V = w.params;
@@ -252,7 +268,8 @@ static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStr
   Timed t(1, s);
   hipError_t e =
       g.variant == kMfma  ? launch_pass1_mfma(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s)
-      : g.variant == kX32 ? launch_pass1_x32(g, X, w.x, w.ln2, ln_out, w.lnsum, s)
+      : (g.variant == kX32 || g.variant == kMixed)
+          ? launch_pass1_x32(g, X, w.x, w.ln2, ln_out, w.lnsum, s)
                           : launch_pass1_valu(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s);
   return check_hip(e, "pass 1 (log-normalizer)");
 }
@@ -260,7 +277,8 @@ static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStr
 static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
   Timed t(2, s);
   hipError_t e =
-      g.variant == kMfma  ? launch_pass2_mfma(g, X, w.params, w.bias, w.ln2, w.part, s)
+      (g.variant == kMfma || g.variant == kMixed)
+          ? launch_pass2_mfma(g, X, w.params, w.bias, w.ln2, w.part, s)
       : g.variant == kX32 ? launch_pass2_x32(g, X, w.x, w.ln2, w.part, s)
                           : launch_pass2_valu(g, X, w.params, w.bias, w.ln2, w.part, s);
   return check_hip(e, "pass 2 (sufficient statistics)");
@@ -269,7 +287,11 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
 // Entry points without an x32 form (the gamma-returning E-steps, whose
 // candidate scheme would pay off only when gamma is consumed on chip, and
 // Pass 2 from a caller's log-normalizer) run the fp64 matrix-core path.
-static int estep_variant(int variant) { return variant == kX32 ? kMfma : variant; }
+static int estep_variant(int K, int d, int variant) {
+  if (variant < 0 || variant > kMixed) return variant;   // rejected by validate_shape
+  variant = resolve_variant(K, d, variant);
+  return (variant == kX32 || variant == kMixed) ? kMfma : variant;
+}
 
 // Standard E-step workspace: the common regions, then the fp64 matrix L.
 static size_t lmat_offset(const WsLayout& L) { return L.total; }
@@ -369,7 +391,7 @@ int fgmm_accumulate_stats(const float* X, const float* mu, const float* var,
   g_err[0] = 0;
   // x32's Pass 2 needs its own Pass 1 (window anchors, slots); with a caller's
   // log-normalizer the fp64 matrix-core pass runs instead
-  variant = estep_variant(variant);
+  variant = estep_variant(K, d, variant);
   int rc = validate_shape(N, K, d, variant);
   if (rc) return rc;
   FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
@@ -434,7 +456,7 @@ int fgmm_flash_e_step(const float* X, const float* mu, const float* var, const f
                       long N, int K, int d, int variant, float* gamma, float* log_normalizer,
                       void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
-  variant = estep_variant(variant);
+  variant = estep_variant(K, d, variant);
   int rc = validate_shape(N, K, d, variant);
   if (rc) return rc;
   FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
@@ -452,7 +474,7 @@ int fgmm_flash_e_step(const float* X, const float* mu, const float* var, const f
 }
 
 size_t fgmm_standard_e_step_workspace_bytes(long N, int K, int d, int variant) {
-  variant = estep_variant(variant);
+  variant = estep_variant(K, d, variant);
   if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
   Geom g = make_geom(N, K, d, variant);
   return std_estep_bytes(g, make_layout(g));
@@ -462,7 +484,7 @@ int fgmm_standard_e_step(const float* X, const float* mu, const float* var,
                          const float* log_pi, long N, int K, int d, int variant, float* gamma,
                          float* log_normalizer, void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
-  variant = estep_variant(variant);
+  variant = estep_variant(K, d, variant);
   int rc = validate_shape(N, K, d, variant);
   if (rc) return rc;
   FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);

@@ -61,7 +61,13 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
   const bool real = (m != nullptr);
   double lnv = 0.0, q = 0.0;
   const int Q = dp / 4, S1 = dp / 2;
-  float* P32 = reinterpret_cast<float*>(P + 2 * (size_t)Kp * dp);
+  const bool mf = variant == kMfma || variant == kMixed;   // fp64 fragment set
+  const bool xf = variant == kX32 || variant == kMixed;    // x32 set
+  // kMixed keeps the x32 set behind the fp64 fragment set (and its direct
+  // bias behind the expanded one)
+  double* Vx = variant == kMixed ? P + 2 * (size_t)Kp * dp : P;
+  float* P32 = reinterpret_cast<float*>(Vx + 2 * (size_t)Kp * dp);
+  double* bx = variant == kMixed ? bias + Kp : bias;
   for (int j = threadIdx.x; j < dp; j += blockDim.x) {
     double iv = 0.0, mu = 0.0;
     if (real && j < d) {
@@ -73,19 +79,21 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
     }
     const int ks = k >> 4, c = k & 15, g = j / Q, t = j - g * Q;
     const int lane = 16 * g + c;
-    if (variant == kMfma) {
+    if (mf) {
       P[((size_t)ks * S1 + t) * 64 + lane] = -0.5 * kLog2e * iv;
       P[((size_t)ks * S1 + Q + t) * 64 + lane] = kLog2e * mu * iv;
-    } else if (variant == kX32) {
+    }
+    if (xf) {
       double sc = sqrt(0.5 * kLog2e * iv);
-      P[2 * ((size_t)k * dp + j)] = sc;
-      P[2 * ((size_t)k * dp + j) + 1] = mu * sc;
-    } else {
+      Vx[2 * ((size_t)k * dp + j)] = sc;
+      Vx[2 * ((size_t)k * dp + j) + 1] = mu * sc;
+    }
+    if (variant == kValu) {
       double sc = sqrt(0.5 * kLog2e * iv);
       P[(size_t)k * dp + j] = sc;
       P[(size_t)Kp * dp + (size_t)k * dp + j] = mu * sc;
     }
-    if (variant == kX32) {
+    if (xf) {
       P32[((size_t)ks * S1 + t) * 64 + lane] = (float)(-0.5 * kLog2e * iv);
       P32[((size_t)ks * S1 + Q + t) * 64 + lane] = (float)(kLog2e * mu * iv);
     }
@@ -93,18 +101,20 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
   lnv = block_sum_f64(lnv, red);
   q = block_sum_f64(q, red);
   if (threadIdx.x == 0) {
-    float* bias32 = reinterpret_cast<float*>(bias + Kp);
+    float* bias32 = reinterpret_cast<float*>(bx + Kp);
     float* Z32 = bias32 + Kp;
     if (!real) {
       bias[k] = -INFINITY;
-      if (variant == kX32) {
+      if (xf) {
+        bx[k] = -INFINITY;
         bias32[k] = -INFINITY;
         Z32[k] = 0.f;
       }
     } else {
       double lc = (double)lp - 0.5 * ((double)d * kLog2Pi + lnv);
-      bias[k] = (variant == kMfma) ? kLog2e * (lc - 0.5 * q) : kLog2e * lc;
-      if (variant == kX32) {
+      bias[k] = mf ? kLog2e * (lc - 0.5 * q) : kLog2e * lc;
+      if (xf) {
+        bx[k] = kLog2e * lc;
         const double be = kLog2e * (lc - 0.5 * q);
         bias32[k] = (float)be;
         // |bias| + D_k, D_k = 0.5 log2(e) sum mu^2/var; rounded up to fp32

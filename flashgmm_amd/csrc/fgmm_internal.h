@@ -28,7 +28,9 @@ constexpr double kLog2Pi = 1.8378770664093454835606594728112;  // ln(2*pi)
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline long round_up_l(long x, long m) { return (x + m - 1) / m * m; }
 
-enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3 };
+// kMixed: the x32 Pass 1 (exact log-normalizer from fp32 matrix-core
+// candidates) with the fp64 matrix-core Pass 2 (no slots, no guard needed).
+enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3, kMixed = 4 };
 
 // What a sweep of the Pass-1 kernels over all components produces per point:
 // the log-normalizer (online log-sum-exp), gamma[n][k] from a known
@@ -41,7 +43,7 @@ struct Geom {
   int K, d;
   int dp;       // d padded to a multiple of 16
   int Kp;       // K padded to a multiple of 16
-  int variant;  // resolved (kValu, kMfma or kX32)
+  int variant;  // resolved (kValu, kMfma, kX32 or kMixed)
   // pass 1
   int p1_blocks;
   // pass 2

@@ -298,17 +298,21 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   const double l2 = eM + log2(eS);
   const double lnat = l2 * kLn2;
   if (valid) {
-    const size_t base = (size_t)n * kSlots + 4 * g;
+    if (ck != nullptr) {   // the slots and window data feed the x32 Pass 2 only
+      const size_t base = (size_t)n * kSlots + 4 * g;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      ck[base + q] = sk4[q] >= 0 ? (unsigned short)sk4[q] : kNoSlot;
-      cg[base + q] = sk4[q] >= 0 ? exp2f((float)(sv[q] - l2)) : 0.f;
+      for (int q = 0; q < 4; q++) {
+        ck[base + q] = sk4[q] >= 0 ? (unsigned short)sk4[q] : kNoSlot;
+        cg[base + q] = sk4[q] >= 0 ? exp2f((float)(sv[q] - l2)) : 0.f;
+      }
+      if (g == 0) {
+        m32[n] = Mrun;
+        xm[n] = xmax2;
+      }
     }
     if (g == 0) {
       ln2[n] = l2;
       if (ln_out != nullptr) ln_out[n] = (float)lnat;
-      m32[n] = Mrun;
-      xm[n] = xmax2;
     }
   }
   double contrib = (valid && g == 0) ? lnat : 0.0;

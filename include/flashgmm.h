@@ -25,8 +25,9 @@
  *
  * variant: FGMM_VARIANT_AUTO picks a kernel family from a table keyed by
  * (K, d); FGMM_VARIANT_VALU (fp64 vector ALU), FGMM_VARIANT_MFMA (fp64
- * matrix-core distance) or FGMM_VARIANT_X32 (fp32 matrix-core distance with
- * the significant pairs recomputed in fp64) force one.
+ * matrix-core distance), FGMM_VARIANT_X32 (fp32 matrix-core distance with
+ * the significant pairs recomputed in fp64) or FGMM_VARIANT_MIXED (the x32
+ * log-normalizer pass with the fp64 statistics pass) force one.
  */
 #ifndef FLASHGMM_H
 #define FLASHGMM_H
@@ -46,6 +47,7 @@ extern "C" {
 #define FGMM_VARIANT_VALU 1
 #define FGMM_VARIANT_MFMA 2
 #define FGMM_VARIANT_X32 3   /* fp32 matrix-core distance + exact fp64 refinement */
+#define FGMM_VARIANT_MIXED 4 /* x32 Pass 1 (exact log-normalizer) + fp64 MFMA Pass 2 */
 
 /* Library ABI version (major*100 + minor). */
 int fgmm_version(void);

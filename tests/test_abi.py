@@ -47,8 +47,10 @@ def test_python_signatures_cover_header():
 
 def test_version_and_variant_table(lib):
     assert lib.fgmm_version() >= 100
-    # matrix cores from K >= 16 and d <= 128, vector ALU otherwise
-    assert lib.fgmm_resolve_variant(65536, 256, 128, 0) == 2
+    # matrix cores from K >= 16 and d <= 128 (with the x32 log-normalizer
+    # pass from K >= 256), vector ALU otherwise
+    assert lib.fgmm_resolve_variant(65536, 256, 128, 0) == 4
+    assert lib.fgmm_resolve_variant(262144, 128, 64, 0) == 2
     assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 1
     assert lib.fgmm_resolve_variant(4096, 64, 200, 0) == 1
     assert lib.fgmm_resolve_variant(4096, 8, 32, 2) == 2
@@ -56,8 +58,8 @@ def test_version_and_variant_table(lib):
 
 def test_workspace_bytes(lib):
     for N, K, d in ((4096, 8, 32), (65536, 256, 128), (1048576, 512, 128), (1, 1, 1), (5, 3, 256)):
-        for v in (0, 1, 2):
-            if v == 2 and d > 128:
+        for v in (0, 1, 2, 4):
+            if v in (2, 4) and d > 128:
                 assert lib.fgmm_workspace_bytes(N, K, d, v) == 0
                 continue
             b = lib.fgmm_workspace_bytes(N, K, d, v)
@@ -69,7 +71,8 @@ def test_workspace_bytes(lib):
 
 def test_estep_workspace_bytes(lib):
     for N, K, d in ((4096, 8, 32), (65536, 256, 128), (5, 3, 256), (1, 1, 1)):
-        base = lib.fgmm_workspace_bytes(N, K, d, 0)
+        # the E-steps run the fp64 matrix-core (or vector) layout
+        base = lib.fgmm_workspace_bytes(N, K, d, 2 if (d <= 128 and K >= 16) else 1)
         std = lib.fgmm_standard_e_step_workspace_bytes(N, K, d, 0)
         assert std % 256 == 0 and std >= base + 8 * N * K   # + the fp64 N x K matrix
         # x32 has no gamma-returning form: it runs as the MFMA path
@@ -114,6 +117,7 @@ def test_argument_errors_before_device_work(lib):
     assert _em(lib, d=257) == 1 and b"d must be" in lib.fgmm_last_error()
     assert _em(lib, d=200, variant=2) == 1 and b"MFMA" in lib.fgmm_last_error()
     assert _em(lib, variant=7) == 1 and b"variant" in lib.fgmm_last_error()
+    assert _em(lib, d=200, variant=4) == 1 and b"mixed" in lib.fgmm_last_error()
     for i in range(8):
         assert _em(lib, null=i) == 1 and b"must not be NULL" in lib.fgmm_last_error()
     assert _em(lib, ws=None) == 2 and b"NULL" in lib.fgmm_last_error()

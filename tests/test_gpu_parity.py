@@ -26,7 +26,7 @@ CASES = [(1, None), (2, None), (3, None), (4, None), (5, 131072)]
 def variants_for(K, d):
     v = ["valu"]
     if d <= 128:
-        v += ["mfma", "x32"]
+        v += ["mfma", "x32", "mixed"]
     return v
 
 
@@ -76,7 +76,7 @@ def test_golden_vectors(cuda, name):
     with np.load(path, allow_pickle=False) as z:
         g = {k: z[k] for k in z.files}
     t = to_dev(cuda, g["X"], g["mu"], g["var"], g["log_pi"])
-    for variant in ("valu", "mfma", "x32"):
+    for variant in ("valu", "mfma", "x32", "mixed"):
         print(f"[case] golden {name} variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], g["ln"], f"{name} {variant}")
@@ -227,7 +227,7 @@ def test_unaligned_and_noncontiguous_inputs(cuda):
     Xu = big[1:].view(X.shape)                    # 4-byte offset: scalar load path
     assert Xu.data_ptr() % 16 != 0
     t = to_dev(cuda, mu, var, lp)
-    for variant in ("valu", "mfma", "x32"):
+    for variant in ("valu", "mfma", "x32", "mixed"):
         print(f"[case] unaligned X variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(Xu, *t, variant=variant)]
         check_params(out[:3], ref[:3], f"unaligned {variant}")
@@ -284,7 +284,7 @@ def test_x32_starved_component_takes_exact_path(cuda):
     ref = O.c_m_step_update(n_k, s_k, sq_k, N)
     assert 1e-9 < n_k[4] < 1e-8, n_k[4]      # starved, at the clamp
     t = to_dev(cuda, X, mu, var, lp)
-    for variant in ("x32", "mfma"):
+    for variant in ("x32", "mixed", "mfma"):
         print(f"[case] starved component variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], ln, f"starved {variant}")
@@ -304,7 +304,7 @@ def test_x32_crowded_window_overflows_slots(cuda):
     lp = np.full(K, -np.log(K), np.float32)
     ref = O.c_em_fused(X, mu, var, lp)
     t = to_dev(cuda, X, mu, var, lp)
-    for variant in ("x32", "mfma"):
+    for variant in ("x32", "mixed", "mfma"):
         print(f"[case] crowded window variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], ref[3], f"crowded {variant}")
