@@ -27,8 +27,10 @@ namespace fgmm {
 // VALU layout: P[k*dp + j] = s_kj = sqrt(0.5*log2(e)/var_kj),
 //              P[Kp*dp + k*dp + j] = mu_kj*s_kj,  bias_k = log2(e)*log_coeff_k
 // so that ll2_nk = bias_k - sum_j (x_j*s_kj - mu_kj*s_kj)^2.
-// x32 layout: the same pair interleaved, P[2(k*dp + j)] = s_kj,
-//             P[2(k*dp + j) + 1] = mu_kj*s_kj (one 16-byte load per feature).
+// x32 layout: the same pair interleaved, (s_kj, mu_kj*s_kj) as one 16-byte
+//             element at position k*dp + 4t + g for feature j = g*(dp/4) + t,
+//             so the four lanes that hold a point's feature quarters read
+//             64 contiguous bytes per load.
 // ---------------------------------------------------------------------------
 
 __device__ inline double wave_sum_f64(double v) {
@@ -84,9 +86,11 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
       P[((size_t)ks * S1 + Q + t) * 64 + lane] = kLog2e * mu * iv;
     }
     if (xf) {
+      // quarter-interleaved: feature j = g*Q + t at position 4t + g
       double sc = sqrt(0.5 * kLog2e * iv);
-      Vx[2 * ((size_t)k * dp + j)] = sc;
-      Vx[2 * ((size_t)k * dp + j) + 1] = mu * sc;
+      const size_t pos = (size_t)k * dp + 4 * t + g;
+      Vx[2 * pos] = sc;
+      Vx[2 * pos + 1] = mu * sc;
     }
     if (variant == kValu) {
       double sc = sqrt(0.5 * kLog2e * iv);

@@ -66,8 +66,8 @@ struct WsLayout {
 };
 
 // Coefficient views of the x32 variant (see fgmm_x32.hip).  The params
-// region holds the fp64 direct-form coefficients V2 (interleaved pairs
-// V2[k*dp + j] = (s_kj, mu_kj s_kj)) followed by the fp32 fragment-ordered
+// region holds the fp64 direct-form coefficients V2 ((s_kj, mu_kj s_kj)
+// pairs, quarter-interleaved, see x32_dist) followed by the fp32 fragment-ordered
 // coefficients; the bias region holds the fp64 direct-form bias, the fp32
 // expanded bias and the fp32 per-component error constants Z.
 struct X32Ws {
@@ -97,17 +97,24 @@ constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
 constexpr double kU32 = 5.9604644775390625e-8;  // 2^-24
 __host__ __device__ constexpr double x32_err_c(int dp) { return (2.0 * dp + 8.0) * kU32; }
 
-// sum_{j in [j0, j1)} (x_j s_kj - mu_kj s_kj)^2 in fp64 from the interleaved
-// direct-form coefficients of the x32 variant (V2 pairs, see X32Ws).
-__device__ inline double x32_dist(const float* __restrict__ x, int j0, int j1,
+// sum_j (x_j s_kj - mu_kj s_kj)^2 over j < d in fp64 from the direct-form
+// coefficients of the x32 variant: V2 holds (s, mu s) pairs, feature
+// j = g*(dp/4) + t at position k*dp + 4t + g (quarter-interleaved).
+__device__ inline double x32_dist(const float* __restrict__ x, int d,
                                   const double* __restrict__ V2, int dp, int k) {
   const double2* c = reinterpret_cast<const double2*>(V2) + (size_t)k * dp;
+  const int Q = dp >> 2;
   double acc = 0.0;
-#pragma unroll 4
-  for (int j = j0; j < j1; j++) {
-    const double2 sm = c[j];
-    const double t = fma((double)x[j], sm.x, -sm.y);
-    acc = fma(t, t, acc);
+  for (int t = 0; t < Q; t++) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int j = g * Q + t;
+      if (j < d) {
+        const double2 sm = c[4 * t + g];
+        const double u = fma((double)x[j], sm.x, -sm.y);
+        acc = fma(u, u, acc);
+      }
+    }
   }
   return acc;
 }
@@ -117,7 +124,7 @@ __device__ inline double x32_dist(const float* __restrict__ x, int j0, int j1,
 __device__ inline double exact_ll2(const float* __restrict__ x, int d,
                                    const double* __restrict__ V2, int dp,
                                    const double* __restrict__ b64, int k) {
-  return b64[k] - x32_dist(x, 0, d, V2, dp, k);
+  return b64[k] - x32_dist(x, d, V2, dp, k);
 }
 
 Geom make_geom(long N, int K, int d, int variant);

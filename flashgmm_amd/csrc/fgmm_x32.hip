@@ -162,10 +162,11 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   double sv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // largest exact pairs (slots)
   int sk4[4] = {-1, -1, -1, -1};
   // Evaluates the pending pairs still inside the window and empties the
-  // lists.  Wavefront-uniform: the four lanes of point c take turns as the
-  // source lane group gs; each computes its quarter of the fp64 distance of
-  // the source's i-th pair, two shuffles complete it, the source lane folds
-  // the exact value into its sums and slots.
+  // lists.  Wavefront-uniform.  The live entries of a point's four lanes
+  // form one queue; round r evaluates every point's r-th entry: its four
+  // lanes each compute their quarter of the fp64 distance, two shuffles
+  // complete it, and the lane whose list held the entry folds the exact value
+  // into its sums and slots.  Rounds = the longest queue in the wavefront.
 #define FGMM_X1_FLUSH(thr_)                                                           \
   {                                                                                   \
     const float th_ = (thr_);                                                         \
@@ -180,42 +181,42 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");                            \
     __builtin_amdgcn_wave_barrier();                                                  \
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");                            \
-    int rounds_ = live_;                                                              \
+    const int c0_ = __shfl(live_, c, 64), c1_ = __shfl(live_, 16 + c, 64);            \
+    const int c2_ = __shfl(live_, 32 + c, 64), c3_ = __shfl(live_, 48 + c, 64);       \
+    const int tot_ = c0_ + c1_ + c2_ + c3_;                                           \
+    int rounds_ = tot_;                                                               \
     _Pragma("unroll") for (int o_ = 32; o_ >= 1; o_ >>= 1)                            \
         rounds_ = max(rounds_, __shfl_xor(rounds_, o_, 64));                          \
-    for (int i_ = 0; i_ < rounds_; i_++) {                                            \
-      _Pragma("unroll") for (int gs_ = 0; gs_ < 4; gs_++) {                           \
-        const int src_ = gs_ * 16 + c;                                                \
-        const bool go_ = i_ < __shfl(live_, src_, 64);                                \
-        if (__ballot(go_) != 0ull) {                                                  \
-          int k_ = 0;                                                                 \
-          double q_ = 0.0;                                                            \
-          if (go_) {                                                                  \
-            k_ = plist[i_ * kThr1 + wave * 64 + src_].x;                              \
-            const double2* cf_ =                                                      \
-                reinterpret_cast<const double2*>(V2) + (size_t)k_ * DP + g * Q;       \
-            _Pragma("unroll") for (int j_ = 0; j_ < Q; j_++) {                        \
-              const double2 sm_ = cf_[j_];                                            \
-              const double t_ = fma((double)xq[j_], sm_.x, -sm_.y);                   \
-              q_ = fma(t_, t_, q_);                                                   \
-            }                                                                         \
-          }                                                                           \
-          q_ += __shfl_xor(q_, 16, 64);                                               \
-          q_ += __shfl_xor(q_, 32, 64);                                               \
-          if (go_ && g == gs_) {                                                      \
-            const double v_ = b64[k_] - q_;                                           \
-            const double mn_ = fmax(eM, v_);                                          \
-            eS = eS * (double)exp2f((float)(eM - mn_)) + (double)exp2f((float)(v_ - mn_)); \
-            eM = mn_;                                                                 \
-            double cv_ = v_;                                                          \
-            int ck_ = k_;                                                             \
-            _Pragma("unroll") for (int q4_ = 0; q4_ < 4; q4_++) {                     \
-              if (cv_ > sv[q4_]) {                                                    \
-                const double tv_ = sv[q4_];                                           \
-                const int tk_ = sk4[q4_];                                             \
-                sv[q4_] = cv_; sk4[q4_] = ck_; cv_ = tv_; ck_ = tk_;                  \
-              }                                                                       \
-            }                                                                         \
+    for (int r_ = 0; r_ < rounds_; r_++) {                                            \
+      const bool go_ = r_ < tot_;                                                     \
+      const int gs_ = r_ < c0_ ? 0 : (r_ < c0_ + c1_ ? 1 : (r_ < c0_ + c1_ + c2_ ? 2 : 3)); \
+      const int i_ = r_ - (gs_ > 0 ? c0_ : 0) - (gs_ > 1 ? c1_ : 0) - (gs_ > 2 ? c2_ : 0); \
+      int k_ = 0;                                                                     \
+      double q_ = 0.0;                                                                \
+      if (go_) {                                                                      \
+        k_ = plist[i_ * kThr1 + wave * 64 + gs_ * 16 + c].x;                          \
+        const double2* cf_ =                                                          \
+            reinterpret_cast<const double2*>(V2) + (size_t)k_ * DP + g;               \
+        _Pragma("unroll") for (int j_ = 0; j_ < Q; j_++) {                            \
+          const double2 sm_ = cf_[4 * j_];                                            \
+          const double t_ = fma((double)xq[j_], sm_.x, -sm_.y);                       \
+          q_ = fma(t_, t_, q_);                                                       \
+        }                                                                             \
+      }                                                                               \
+      q_ += __shfl_xor(q_, 16, 64);                                                   \
+      q_ += __shfl_xor(q_, 32, 64);                                                   \
+      if (go_ && g == gs_) {                                                          \
+        const double v_ = b64[k_] - q_;                                               \
+        const double mn_ = fmax(eM, v_);                                              \
+        eS = eS * (double)exp2f((float)(eM - mn_)) + (double)exp2f((float)(v_ - mn_)); \
+        eM = mn_;                                                                     \
+        double cv_ = v_;                                                              \
+        int ck_ = k_;                                                                 \
+        _Pragma("unroll") for (int q4_ = 0; q4_ < 4; q4_++) {                         \
+          if (cv_ > sv[q4_]) {                                                        \
+            const double tv_ = sv[q4_];                                               \
+            const int tk_ = sk4[q4_];                                                 \
+            sv[q4_] = cv_; sk4[q4_] = ck_; cv_ = tv_; ck_ = tk_;                      \
           }                                                                           \
         }                                                                             \
       }                                                                               \
