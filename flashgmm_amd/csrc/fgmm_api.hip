@@ -42,7 +42,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // the fp64 one by 20-27 % at d = 64 and 128 (measured; at K = 128 its
 // candidate work outweighs the saving), so auto pairs it with the fp64 Pass 2.
 static int resolve_variant(int K, int d, int variant) {
-  if (variant >= kValu && variant <= kMixed) return variant;
+  if (variant >= kValu && variant <= kSparse) return variant;
   if (d <= 128 && K >= 256) return kMixed;
   if (d <= 128 && K >= 16) return kMfma;
   return kValu;
@@ -54,7 +54,7 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.K = K;
   g.d = d;
   g.variant = resolve_variant(K, d, variant);
-  if (g.variant == kMfma || g.variant == kX32 || g.variant == kMixed) {
+  if (g.variant == kMfma || g.variant == kX32 || both_sets(g.variant)) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
     g.p1_blocks = (int)((N + 127) / 128);
@@ -82,20 +82,96 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.p2_chunk = chunk;
   g.p2_chunks = (int)((N + chunk - 1) / chunk);
   g.stat_w = round_up(2 * g.dp + 1, 4);
+  // sparse Pass 2: list capacity per point, sort chunks of kSpPts points
+  g.sp_C = K < kSpCap ? K : kSpCap;
+  g.sp_chunk = kSpPts;
+  g.sp_nchunk = (int)((N + kSpPts - 1) / kSpPts);
   return g;
+}
+
+// Sparse variant's regions behind the common ones, in this order; with a
+// base pointer the views are set as well.  Returns the end offset.
+static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp) {
+  const size_t N = (size_t)g.N, NC = N * (size_t)g.sp_C, Kp = (size_t)g.Kp;
+  const size_t nch = (size_t)g.sp_nchunk, npc = (size_t)sp_npiece_cap(g);
+  auto take = [&](size_t bytes) {
+    char* p = b != nullptr ? b + off : nullptr;
+    off = align256(off + bytes);
+    return p;
+  };
+  char* xm = take(sizeof(float) * N);
+  char* pcnt = take(sizeof(int) * N);
+  char* pk = take(sizeof(int) * NC);
+  char* pv = take(sizeof(double) * NC);
+  char* blk = take(sizeof(int2) * nch * kSpChunkCap);
+  char* ecnt = take(sizeof(int) * nch);
+  char* fcap = take(sizeof(int) * nch);
+  char* cnt = take(sizeof(int) * Kp * nch);
+  char* tsum = take(sizeof(int) * (size_t)sp_ntile(g));
+  char* ocnt = take(sizeof(int) * nch);
+  char* xsum = take(sizeof(double) * nch);
+  char* seg = take(sizeof(int) * (Kp + 1));
+  char* pstart = take(sizeof(int) * (Kp + 1));
+  char* pcomp = take(sizeof(int) * npc);
+  char* nov = take(sizeof(int) * 2);
+  char* glob = take(sizeof(double) * 4);
+  char* sorted = take(sizeof(int2) * NC);
+  char* prow = take(sizeof(double) * npc * (size_t)g.stat_w);
+  char* Xo = take(sizeof(float) * N * (size_t)g.d);
+  char* ln2o = take(sizeof(double) * N);
+  char* part_sp = take(sizeof(double) * Kp * (size_t)g.stat_w);
+  char* kmap = take(sizeof(int) * Kp);
+  char* nflag = take(sizeof(int));
+  char* Pf = take(sizeof(double) * 2 * Kp * (size_t)g.dp);
+  char* biasf = take(sizeof(double) * Kp);
+  char* flag = take(sizeof(int) * Kp);
+  char* dmass = take(sizeof(float) * (size_t)g.p1_blocks * Kp);
+  if (b != nullptr) {
+    x->dmass = reinterpret_cast<float*>(dmass);
+    x->xm = reinterpret_cast<float*>(xm);
+    x->pcnt = reinterpret_cast<int*>(pcnt);
+    x->pk = reinterpret_cast<int*>(pk);
+    x->pv = reinterpret_cast<double*>(pv);
+    x->pC = g.sp_C;
+    x->flag = reinterpret_cast<int*>(flag);
+    sp->xm = x->xm;
+    sp->blk = reinterpret_cast<int2*>(blk);
+    sp->ecnt = reinterpret_cast<int*>(ecnt);
+    sp->fcap = reinterpret_cast<int*>(fcap);
+    sp->cnt = reinterpret_cast<int*>(cnt);
+    sp->tsum = reinterpret_cast<int*>(tsum);
+    sp->ocnt = reinterpret_cast<int*>(ocnt);
+    sp->xsum = reinterpret_cast<double*>(xsum);
+    sp->seg = reinterpret_cast<int*>(seg);
+    sp->pstart = reinterpret_cast<int*>(pstart);
+    sp->pcomp = reinterpret_cast<int*>(pcomp);
+    sp->nov = reinterpret_cast<int*>(nov);
+    sp->glob = reinterpret_cast<double*>(glob);
+    sp->sorted = reinterpret_cast<int2*>(sorted);
+    sp->prow = reinterpret_cast<double*>(prow);
+    sp->Xo = reinterpret_cast<float*>(Xo);
+    sp->ln2o = reinterpret_cast<double*>(ln2o);
+    sp->part_sp = reinterpret_cast<double*>(part_sp);
+    sp->kmap = reinterpret_cast<int*>(kmap);
+    sp->nflag = reinterpret_cast<int*>(nflag);
+    sp->Pf = reinterpret_cast<double*>(Pf);
+    sp->biasf = reinterpret_cast<double*>(biasf);
+  }
+  return off;
 }
 
 WsLayout make_layout(const Geom& g) {
   WsLayout L;
   size_t off = 0;
   const bool x32 = g.variant == kX32;
-  const bool xset = x32 || g.variant == kMixed;        // holds the x32 coefficient set
+  const bool both = both_sets(g.variant);
+  const bool xset = x32 || both;                       // holds the x32 coefficient set
   const size_t kd2 = 2 * (size_t)g.Kp * g.dp;
   L.params = off;
-  off = align256(off + sizeof(double) * kd2 * (g.variant == kMixed ? 2 : 1) +
+  off = align256(off + sizeof(double) * kd2 * (both ? 2 : 1) +
                  (xset ? sizeof(float) * kd2 : 0));
   L.bias = off;
-  off = align256(off + sizeof(double) * (size_t)g.Kp * (g.variant == kMixed ? 2 : 1) +
+  off = align256(off + sizeof(double) * (size_t)g.Kp * (both ? 2 : 1) +
                  (xset ? 2 * sizeof(float) * (size_t)g.Kp : 0));
   L.ln2 = off;
   off = align256(off + sizeof(double) * (size_t)g.N);
@@ -112,6 +188,7 @@ WsLayout make_layout(const Geom& g) {
     off = align256(off + sizeof(float) * kX32Slots * N);        // slot gammas
     off = align256(off + sizeof(int) * (size_t)g.Kp);           // exact-fix flags
   }
+  if (g.variant == kSparse) off = sparse_aux(g, nullptr, off, nullptr, nullptr);
   L.total = off;
   return L;
 }
@@ -163,8 +240,11 @@ static int validate_shape(long N, int K, int d, int variant) {
   if (K > 65536) return fail(FGMM_EINVAL, "K must be <= 65536 (got %d)", K);
   if (d < 1 || d > kMaxD)
     return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
-  if (variant < 0 || variant > kMixed)
+  if (variant < 0 || variant > kSparse)
     return fail(FGMM_EINVAL, "unknown variant %d", variant);
+  if (variant == kSparse && (d > 128 || K > 8192))
+    return fail(FGMM_EINVAL, "the sparse variant supports d <= 128 and K <= 8192 (got d=%d, K=%d)",
+                d, K);
   if (variant == kMixed && d > 128)
     return fail(FGMM_EINVAL, "the mixed variant supports d <= 128 (got %d)", d);
   if (variant == kMfma && d > 128)
@@ -195,6 +275,7 @@ struct Ws {
   double* lnsum;
   double* part;
   X32Ws x;
+  SpWs sp;
   bool layout_ok;
 };
 
@@ -202,8 +283,8 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
   char* b = static_cast<char*>(ws);
   Ws w{reinterpret_cast<double*>(b + L.params), reinterpret_cast<double*>(b + L.bias),
        reinterpret_cast<double*>(b + L.ln2), reinterpret_cast<double*>(b + L.lnsum),
-       reinterpret_cast<double*>(b + L.part), X32Ws{}, true};
-  if (g.variant == kMixed) {   // x32 set behind the fp64 one; no slots
+       reinterpret_cast<double*>(b + L.part), X32Ws{}, SpWs{}, true};
+  if (both_sets(g.variant)) {   // x32 set behind the fp64 one; no slots
     const size_t kd2 = 2 * (size_t)g.Kp * g.dp;
     w.x.V = w.params + kd2;
     w.x.P32 = reinterpret_cast<const float*>(w.params + 2 * kd2);
@@ -231,6 +312,8 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
     off = align256(off + sizeof(int) * (size_t)g.Kp);
     w.layout_ok = (off == L.total);   // the carve must end where the layout does
   }
+  if (g.variant == kSparse)
+    w.layout_ok = sparse_aux(g, b, L.aux, &w.x, &w.sp) == L.total;
   return w;
 }
 
@@ -240,6 +323,26 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
 static int run_reduce(const Geom& g, const float* X, Ws& w, float* mu, float* var, float* lp,
                       double* params_next, double* bias_next, double* ll_out, hipStream_t s) {
   Timed t(3, s);
+  if (g.variant == kSparse) {
+    // stage 1 over the listed pairs' row and the overflow points' dense rows
+    int rc = check_hip(launch_reduce_sparse(g, w.sp.part_sp, 1, w.part, w.sp.nov, g.p2_chunk,
+                                            w.lnsum, mu, var, lp, params_next, bias_next,
+                                            ll_out, s, kReduceFlagging, w.x.flag),
+                       "reduction / M-step");
+    if (rc) return rc;
+    // flagged components: all points, fp64 matrix cores, rows [s][k] of w.part
+    rc = check_hip(launch_flag_compact(g, w.x.flag, w.params, w.bias, w.sp, s),
+                   "flagged components (sparse)");
+    if (rc) return rc;
+    rc = check_hip(launch_pass2_mfma_map(g, X, w.sp.Pf, w.sp.biasf, w.ln2, w.part, w.sp.kmap,
+                                         w.sp.nflag, s),
+                   "exact statistics (sparse)");
+    if (rc) return rc;
+    return check_hip(launch_reduce_sparse(g, w.part, g.p2_chunks, nullptr, nullptr, 0, w.lnsum,
+                                          mu, var, lp, params_next, bias_next, nullptr, s,
+                                          kReduceFlagged, w.x.flag),
+                     "reduction / M-step (exact components)");
+  }
   if (g.variant != kX32)
     return check_hip(launch_reduce(g, w.part, w.lnsum, nullptr, nullptr, nullptr, mu, var, lp,
                                    params_next, bias_next, ll_out, s),
@@ -268,7 +371,7 @@ static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStr
   Timed t(1, s);
   hipError_t e =
       g.variant == kMfma  ? launch_pass1_mfma(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s)
-      : (g.variant == kX32 || g.variant == kMixed)
+      : (g.variant == kX32 || both_sets(g.variant))
           ? launch_pass1_x32(g, X, w.x, w.ln2, ln_out, w.lnsum, s)
                           : launch_pass1_valu(g, X, w.params, w.bias, w.ln2, ln_out, w.lnsum, s);
   return check_hip(e, "pass 1 (log-normalizer)");
@@ -276,6 +379,14 @@ static int run_pass1(const Geom& g, const float* X, Ws& w, float* ln_out, hipStr
 
 static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
   Timed t(2, s);
+  if (g.variant == kSparse) {
+    int rc = check_hip(launch_pass2_sparse(g, X, w.x, w.sp, w.ln2, s),
+                       "pass 2 (sparse statistics)");
+    if (rc) return rc;
+    return check_hip(launch_pass2_mfma_dyn(g, w.sp.Xo, w.params, w.bias, w.sp.ln2o, w.part,
+                                           w.sp.nov, s),
+                     "pass 2 (overflow points)");
+  }
   hipError_t e =
       (g.variant == kMfma || g.variant == kMixed)
           ? launch_pass2_mfma(g, X, w.params, w.bias, w.ln2, w.part, s)
@@ -288,9 +399,9 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
 // candidate scheme would pay off only when gamma is consumed on chip, and
 // Pass 2 from a caller's log-normalizer) run the fp64 matrix-core path.
 static int estep_variant(int K, int d, int variant) {
-  if (variant < 0 || variant > kMixed) return variant;   // rejected by validate_shape
+  if (variant < 0 || variant > kSparse) return variant;   // rejected by validate_shape
   variant = resolve_variant(K, d, variant);
-  return (variant == kX32 || variant == kMixed) ? kMfma : variant;
+  return (variant == kX32 || both_sets(variant)) ? kMfma : variant;
 }
 
 // Standard E-step workspace: the common regions, then the fp64 matrix L.
@@ -324,7 +435,11 @@ static int validate_ws_bytes(void* ws, size_t bytes, size_t need) {
 static size_t stream_acc_bytes(const Geom& g) {
   return align256(sizeof(double) * ((size_t)g.Kp * g.stat_w + 1));
 }
-static int stream_variant(int variant) { return variant == kX32 ? kMfma : variant; }
+static int stream_variant(int K, int d, int variant) {
+  if (variant < 0 || variant > kSparse) return variant;   // rejected by validate_shape
+  variant = resolve_variant(K, d, variant);
+  return variant == kX32 ? kMfma : variant == kSparse ? kMixed : variant;
+}
 
 }  // namespace fgmm
 
@@ -550,7 +665,7 @@ static size_t stream_chunk_bytes(long chunk_rows, int K, int d, int variant) {
 }
 
 size_t fgmm_stream_workspace_bytes(long chunk_rows, int K, int d, int variant) {
-  variant = stream_variant(variant);
+  variant = stream_variant(K, d, variant);
   if (validate_shape(chunk_rows, K, d, variant) != FGMM_OK) return 0;
   Geom g = make_geom(chunk_rows, K, d, variant);
   return stream_acc_bytes(g) + stream_chunk_bytes(chunk_rows, K, d, variant);
@@ -580,7 +695,7 @@ static int stream_setup(long rows, long chunk_rows, int K, int d, int variant, v
 int fgmm_stream_begin(const float* mu, const float* var, const float* log_pi, long chunk_rows,
                       int K, int d, int variant, void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
-  variant = stream_variant(variant);
+  variant = stream_variant(K, d, variant);
   FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
   Geom g;
   Ws w;
@@ -596,7 +711,7 @@ int fgmm_stream_begin(const float* mu, const float* var, const float* log_pi, lo
 int fgmm_stream_chunk(const float* X, long rows, long chunk_rows, int K, int d, int variant,
                       float* log_normalizer, void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
-  variant = stream_variant(variant);
+  variant = stream_variant(K, d, variant);
   FGMM_REQUIRE(X);
   Geom g;
   Ws w;
@@ -614,7 +729,7 @@ int fgmm_stream_end(long N, long chunk_rows, int K, int d, int variant, float* n
                     float* new_var, float* new_log_pi, double* ll_mean, void* ws,
                     size_t ws_bytes, void* stream) {
   g_err[0] = 0;
-  variant = stream_variant(variant);
+  variant = stream_variant(K, d, variant);
   FGMM_REQUIRE(new_mu); FGMM_REQUIRE(new_var); FGMM_REQUIRE(new_log_pi);
   if (N < 1) return fail(FGMM_EINVAL, "N must be >= 1 (got %ld)", N);
   Geom gc;

@@ -63,13 +63,13 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
   const bool real = (m != nullptr);
   double lnv = 0.0, q = 0.0;
   const int Q = dp / 4, S1 = dp / 2;
-  const bool mf = variant == kMfma || variant == kMixed;   // fp64 fragment set
-  const bool xf = variant == kX32 || variant == kMixed;    // x32 set
-  // kMixed keeps the x32 set behind the fp64 fragment set (and its direct
-  // bias behind the expanded one)
-  double* Vx = variant == kMixed ? P + 2 * (size_t)Kp * dp : P;
+  const bool mf = variant == kMfma || both_sets(variant);   // fp64 fragment set
+  const bool xf = variant == kX32 || both_sets(variant);    // x32 set
+  // kMixed and kSparse keep the x32 set behind the fp64 fragment set (and its
+  // direct bias behind the expanded one)
+  double* Vx = both_sets(variant) ? P + 2 * (size_t)Kp * dp : P;
   float* P32 = reinterpret_cast<float*>(Vx + 2 * (size_t)Kp * dp);
-  double* bx = variant == kMixed ? bias + Kp : bias;
+  double* bx = both_sets(variant) ? bias + Kp : bias;
   for (int j = threadIdx.x; j < dp; j += blockDim.x) {
     double iv = 0.0, mu = 0.0;
     if (real && j < d) {
@@ -180,7 +180,8 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               float* __restrict__ new_log_pi,
                               double* __restrict__ P_next, double* __restrict__ bias_next,
                               double* __restrict__ ll_out, int standard, int stage,
-                              int* __restrict__ flag) {
+                              int* __restrict__ flag, const double* __restrict__ part2,
+                              const int* __restrict__ ndyn, long chunk2) {
   __shared__ double red[16];
   __shared__ double nk_sh;
   __shared__ double errb_sh[3];
@@ -206,11 +207,18 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
 
   const size_t row = (size_t)stat_w;
   const size_t kstride = (size_t)Kp * row;
+  // sparse variant: partial rows of the dense pass over the overflow points
+  int S2 = 0;
+  if (part2 != nullptr) S2 = (int)(((long)*ndyn + chunk2 - 1) / chunk2);
   {
     // n_k: chunk partials split across the block, merged in a fixed order
     double t = 0.0;
     const double* p = part + (size_t)k * row + 2 * dp;
     for (int s = threadIdx.x; s < S; s += blockDim.x) t += p[(size_t)s * kstride];
+    if (S2 > 0) {
+      const double* p2 = part2 + (size_t)k * row + 2 * dp;
+      for (int s = threadIdx.x; s < S2; s += blockDim.x) t += p2[(size_t)s * kstride];
+    }
     t = block_sum_f64(t, red);
     if (stage == kReduceFlagging) {
       for (int c = 1; c <= 3; c++) {
@@ -236,6 +244,13 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     for (int s = 0; s < S; s++) {
       a += p[(size_t)s * kstride + j];
       b += p[(size_t)s * kstride + dp + j];
+    }
+    if (S2 > 0) {
+      const double* p2 = part2 + (size_t)k * row;
+      for (int s = 0; s < S2; s++) {
+        a += p2[(size_t)s * kstride + j];
+        b += p2[(size_t)s * kstride + dp + j];
+      }
     }
     sa_sh[j] = a;
     sb_sh[j] = b;
@@ -298,7 +313,23 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
-                     bias_next, ll_out, standard, stage, flag);
+                     bias_next, ll_out, standard, stage, flag, nullptr, nullptr, 1L);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const double* part2,
+                                const int* ndyn, long chunk2, const double* lnsum,
+                                float* new_mu, float* new_var, float* new_log_pi,
+                                double* params_next, double* bias_next, double* ll_out,
+                                hipStream_t s, int stage, int* flag) {
+  if (g.variant != kSparse || stage == kReduceAll || flag == nullptr || S < 1 ||
+      g.stat_w < 2 * g.dp + 4 || (part2 != nullptr && (ndyn == nullptr || chunk2 < 1)))
+    return hipErrorInvalidValue;
+  const int blocks = (params_next != nullptr || stage == kReduceFlagging) ? g.Kp : g.K;
+  hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
+                     g.Kp, g.d, g.dp, S, g.stat_w, part, lnsum, g.p1_blocks, nullptr,
+                     nullptr, nullptr, new_mu, new_var, new_log_pi, params_next, bias_next,
+                     ll_out, 0, stage, flag, part2, ndyn, chunk2 < 1 ? 1L : chunk2);
   return hipGetLastError();
 }
 

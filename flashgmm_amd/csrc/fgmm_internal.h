@@ -30,7 +30,12 @@ inline long round_up_l(long x, long m) { return (x + m - 1) / m * m; }
 
 // kMixed: the x32 Pass 1 (exact log-normalizer from fp32 matrix-core
 // candidates) with the fp64 matrix-core Pass 2 (no slots, no guard needed).
-enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3, kMixed = 4 };
+// kSparse: the x32 Pass 1 also lists every exactly evaluated pair per point;
+// Pass 2 accumulates the statistics from those lists alone (fgmm_sparse.hip).
+enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3, kMixed = 4, kSparse = 5 };
+// Variants that keep both the fp64 fragment-ordered coefficient set and the
+// x32 set behind it.
+__host__ __device__ inline bool both_sets(int v) { return v == kMixed || v == kSparse; }
 
 // What a sweep of the Pass-1 kernels over all components produces per point:
 // the log-normalizer (online log-sum-exp), gamma[n][k] from a known
@@ -43,7 +48,7 @@ struct Geom {
   int K, d;
   int dp;       // d padded to a multiple of 16
   int Kp;       // K padded to a multiple of 16
-  int variant;  // resolved (kValu, kMfma, kX32 or kMixed)
+  int variant;  // resolved (kValu, kMfma, kX32, kMixed or kSparse)
   // pass 1
   int p1_blocks;
   // pass 2
@@ -51,6 +56,10 @@ struct Geom {
   int p2_chunks;    // grid.y (S): point chunks, one stats partial each
   long p2_chunk;    // points per chunk (multiple of the point tile)
   int stat_w;       // row width of a stats partial (2*dp + 1 padded to 4)
+  // sparse Pass 2
+  int sp_C;         // list entries per point (more: the point takes the dense path)
+  long sp_chunk;    // points per sort chunk
+  int sp_nchunk;
 };
 
 // Byte offsets of the workspace regions (all 256-byte aligned).
@@ -81,8 +90,58 @@ struct X32Ws {
   unsigned short* ck;  // [N][kX32Slots] slot components (0xFFFF = empty)
   float* cg;           // [N][kX32Slots] slot responsibilities (exact)
   int* flag;           // [Kp] components whose statistics are recomputed exactly
+  // sparse variant: per-point pair lists written by Pass 1
+  int* pk;             // [N][pC] component
+  double* pv;          // [N][pC] exact ll2
+  int* pcnt;           // [N] entries of the point (> pC: the list overflowed)
+  int pC;
+  float* dmass;        // [Kp][p1_blocks] bound on the unlisted responsibility mass
 };
 constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
+
+// Sparse variant.  Pass 1 lists every pair it evaluates exactly (those whose
+// fp32 upper bound reaches within 40 bits of the point's best lower bound, and
+// pending pairs down to 126 bits below it) and bounds, per component, the
+// responsibility of the pairs it leaves out: sum of 2^(upper bound - running
+// max) over them, plus 2^-126 per point for pairs below that.
+constexpr double kSpFloor = 0x1p-126;
+constexpr int kSpCap = 32;            // list entries per point (at most K)
+constexpr int kSpPts = 256;           // points per sort chunk
+constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
+constexpr int kSpPiece = 256;         // entries per accumulation piece
+constexpr int kSpScanTile = 4096;     // counters per scan tile
+
+// Buffers of the sparse Pass 2 (see fgmm_sparse.hip).
+struct SpWs {
+  float* xm;           // [N] max_j x_nj^2 (Pass 1)
+  int2* blk;           // [nchunk][kSpChunkCap] chunk entries sorted by (component, point)
+  int* ecnt;           // [nchunk] entries of the chunk
+  int* fcap;           // [nchunk] first point of the chunk cut by the chunk capacity
+  int* cnt;            // [Kp][nchunk] entries per (component, chunk) -> offsets
+  int* tsum;           // [ntile] scan tile sums -> offsets
+  int* ocnt;           // [nchunk] overflow points per chunk -> offsets
+  double* xsum;        // [nchunk] max xm over the chunk
+  int* seg;            // [Kp + 1] start of each component's entries
+  int* pstart;         // [Kp + 1] first accumulation piece of each component
+  int* pcomp;          // [npiece_cap] component of each piece
+  int* nov;            // [2] overflow points, pieces
+  double* glob;        // [4] N 2^-126, max_n max_j |x_nj|, its square
+  int2* sorted;        // [N * C] (point, float gamma bits) by (component, point)
+  double* prow;        // [npiece_cap][stat_w] piece sums
+  float* Xo;           // [N][d] rows of the overflow points
+  double* ln2o;        // [N] their log-normalizers
+  double* part_sp;     // [Kp][stat_w] statistics of the listed pairs
+  int* kmap;           // [Kp] flagged components, compacted (-1 = padding)
+  int* nflag;          // [1]
+  double* Pf;          // fp64 fragment coefficients of the flagged components
+  double* biasf;       // [Kp]
+};
+inline int sp_ntile(const Geom& g) {
+  return (int)(((long)g.Kp * g.sp_nchunk + kSpScanTile - 1) / kSpScanTile);
+}
+inline long sp_npiece_cap(const Geom& g) {
+  return (long)g.N * g.sp_C / kSpPiece + g.Kp + 1;
+}
 
 // Error model of the fp32 expanded distance (x32 variant).  ll32 is
 // fl(a0 + a1) with a0 = sum_j P1_kj x_j^2 and a1 = bias_k + sum_j P2_kj x_j
@@ -159,6 +218,33 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s,
                          int standard = 0, int stage = kReduceAll, int* flag = nullptr);
+// Sparse variant: sums S rows of part, then the first ceil(*ndyn / chunk2)
+// rows of part2 (the dense pass over the overflow points; none if part2 is
+// null).  Error-bound columns come from part alone.
+hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const double* part2,
+                                const int* ndyn, long chunk2, const double* lnsum,
+                                float* new_mu, float* new_var, float* new_log_pi,
+                                double* params_next, double* bias_next, double* ll_out,
+                                hipStream_t s, int stage, int* flag);
+// Sparse Pass 2: chunk sort, scan, placement (+ gather of the overflow
+// points), piece sums, fold into sp.part_sp.
+hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, const SpWs& sp,
+                               const double* ln2, hipStream_t s);
+// Flagged components (flag[k] != 0) compacted into sp.kmap / sp.nflag with
+// their fp64 fragment coefficients gathered into sp.Pf / sp.biasf.
+hipError_t launch_flag_compact(const Geom& g, const int* flag, const double* P,
+                               const double* bias, const SpWs& sp, hipStream_t s);
+// fp64 matrix-core Pass 2 over the first *ndyn rows of X (device count, at
+// most g.N); chunks past them exit without writing.
+hipError_t launch_pass2_mfma_dyn(const Geom& g, const float* X, const double* P,
+                                 const double* bias, const double* ln2, double* part,
+                                 const int* ndyn, hipStream_t s);
+// fp64 matrix-core Pass 2 over all points for the compacted components of
+// P/bias (the first *kdyn of them); the row of compact component i is
+// part[s][kmap[i]].
+hipError_t launch_pass2_mfma_map(const Geom& g, const float* X, const double* P,
+                                 const double* bias, const double* ln2, double* part,
+                                 const int* kmap, const int* kdyn, hipStream_t s);
 // Streaming: acc[k][c] += sum_s part[s][k][c] for c < 2dp+1 (fixed order over
 // s), acc_ln[0] += sum of the Pass-1 workgroup sums.
 hipError_t launch_accumulate(const Geom& g, const double* part, const double* lnsum,

@@ -219,11 +219,15 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
 // Each workgroup writes one fp64 partial row [sum gamma*x | sum gamma*x^2 |
 // sum gamma] per component, reduced later in fp64 in a fixed order.
 // ---------------------------------------------------------------------------
-template <int DP, bool VEC>
+// SPLIT: the four wavefronts share one 16-component subtile and take one
+// 16-point quarter of each tile each (for few components, e.g. the flagged
+// ones of the sparse variant); their sums are combined in a fixed order.
+template <int DP, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const double* __restrict__ P,
     const double* __restrict__ bias, const double* __restrict__ ln2,
-    double* __restrict__ part, long chunk, int nchunks, int kblocks, int stat_w) {
+    double* __restrict__ part, long chunk, int nchunks, int kblocks, int stat_w,
+    const int* __restrict__ ndyn, const int* __restrict__ kmap, const int* __restrict__ kdyn) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int XS = DP + 20;  // LDS row stride in floats (16-byte aligned rows)
   constexpr int NFT = DP / 16;
@@ -237,11 +241,23 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
   const int kb = local % kblocks;
   const int chunk_id = (local / kblocks) * 8 + xcd;
   if (chunk_id >= nchunks) return;
+  if (ndyn != nullptr) {   // rows past the device count: no chunk, no partial row
+    const long nd = *ndyn;
+    N = nd < N ? nd : N;
+    if ((long)chunk_id * chunk >= N) return;
+  }
+
+  // compacted components (kdyn): only the first round_up(*kdyn, 16) slots
+  int kact = Kp;
+  if (kdyn != nullptr) {
+    kact = (*kdyn + 15) & ~15;
+    if (kb * (SPLIT ? 1 : kP2Waves) * 16 >= kact) return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int ks = kb * kP2Waves + wave;
-  const bool active = ks < (Kp >> 4);
+  const int ks = SPLIT ? kb : kb * kP2Waves + wave;
+  const bool active = ks < (kact >> 4);
   const long p0 = (long)chunk_id * chunk;
   const long p1 = (p0 + chunk < N) ? p0 + chunk : N;
 
@@ -263,6 +279,7 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     accS[f] = f32x4{0.f, 0.f, 0.f, 0.f};
     accQ[f] = f64x4{0.0, 0.0, 0.0, 0.0};
   }
+  double accD[SPLIT ? NFT : 1][4];   // SPLIT: wave 0's sum gamma x in fp64 after the combine
   double nk = 0.0;
 
   float4 pre[V4];
@@ -330,7 +347,23 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     const int buf = (int)(it & 1);
     const long t0 = p0 + it * kP2Tile;
     if (it + 1 < ntile) gload(t0 + kP2Tile);
-    if (active) {
+    if (SPLIT && active) {   // quarter `wave` of the tile
+      const float* xt = xs[buf];
+      f64x4 a0 = f64x4{bk, bk, bk, bk}, a1 = f64x4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int s4 = 0; s4 < Q / 4; s4++) gemm1_block(xt + (wave * 16 + c) * XS + g * Q, s4, a0, a1);
+      float gm[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const double ll = a0[r] + a1[r];
+        gm[r] = exp2f((float)(ll - ls[buf][wave * 16 + 4 * r + g]));
+        nk += (double)gm[r];
+      }
+      const float* xsub = xt + wave * 16 * XS;
+#pragma unroll
+      for (int p = 0; p < 4 * NFT; p++) gemm2_pair(xsub, gm, p);
+    }
+    if (!SPLIT && active) {
       const float* xt = xs[buf];
       f64x4 a0 = f64x4{bk, bk, bk, bk}, a1 = f64x4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
@@ -367,21 +400,68 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     __syncthreads();
   }
 
-  if (!active) return;
-  double* out = part + ((size_t)chunk_id * Kp + (size_t)ks * 16) * stat_w;
+  if (!active) return;   // workgroup-uniform when SPLIT
+  if (SPLIT) {
+    // waves 1..3 hand their sums to wave 0 through the (now idle) tile buffer
+    constexpr int W = 8 * NFT + 1;   // doubles per lane
+#pragma unroll
+    for (int f = 0; f < NFT; f++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) accD[f][r] = (double)accS[f][r];
+    }
+    double* sc = reinterpret_cast<double*>(&xs[0][0]);
+    for (int w = 1; w < kP2Waves; w++) {
+      if (wave == w) {
+#pragma unroll
+        for (int f = 0; f < NFT; f++) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            sc[lane * W + 8 * f + r] = (double)accS[f][r];
+            sc[lane * W + 8 * f + 4 + r] = accQ[f][r];
+          }
+        }
+        sc[lane * W + 8 * NFT] = nk;
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int f = 0; f < NFT; f++) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            accD[f][r] += sc[lane * W + 8 * f + r];
+            accQ[f][r] += sc[lane * W + 8 * f + 4 + r];
+          }
+        }
+        nk += sc[lane * W + 8 * NFT];
+      }
+      __syncthreads();
+    }
+    if (wave != 0) return;
+  }
+  // partial row of local component R (kmap: the compacted slot's component,
+  // -1 for padding)
+  auto row = [&](int R) -> double* {
+    const int kr = kmap != nullptr ? kmap[ks * 16 + R] : ks * 16 + R;
+    return kr < 0 ? nullptr : part + ((size_t)chunk_id * Kp + (size_t)kr) * stat_w;
+  };
   // fp32 16x16x4 accumulator: register r of lane (g, c) is row 4g+r;
   // fp64 16x16x4 accumulator: register r of lane (g, c) is row 4r+g.
 #pragma unroll
-  for (int f = 0; f < NFT; f++) {
+  for (int r = 0; r < 4; r++) {
+    double* oS = row(4 * g + r);
+    double* oQ = row(4 * r + g);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      out[(size_t)(4 * g + r) * stat_w + f * 16 + c] = (double)accS[f][r];
-      out[(size_t)(4 * r + g) * stat_w + DP + f * 16 + c] = accQ[f][r];
+    for (int f = 0; f < NFT; f++) {
+      if (oS != nullptr) oS[f * 16 + c] = SPLIT ? accD[f][r] : (double)accS[f][r];
+      if (oQ != nullptr) oQ[DP + f * 16 + c] = accQ[f][r];
     }
   }
   nk += __shfl_xor(nk, 16, 64);
   nk += __shfl_xor(nk, 32, 64);
-  if (g == 0) out[(size_t)c * stat_w + 2 * DP] = nk;
+  if (g == 0) {
+    double* o = row(c);
+    if (o != nullptr) o[2 * DP] = nk;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -423,11 +503,19 @@ static hipError_t p1_sweep(const Geom& g, bool v, int sweep, const float* X, con
 template <int DP, bool VEC>
 static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
                             const double* bias, const double* ln2, double* part,
-                            hipStream_t s) {
+                            hipStream_t s, const int* ndyn = nullptr,
+                            const int* kmap = nullptr, const int* kdyn = nullptr) {
   const int padded = (g.p2_chunks + 7) / 8 * 8;
-  hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC>), dim3(g.p2_kblocks * padded),
+  if (kmap != nullptr) {   // compacted components: one 16-component subtile per workgroup
+    const int kblocks = g.Kp / 16;
+    hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, true>), dim3(kblocks * padded),
+                       dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
+                       g.p2_chunk, g.p2_chunks, kblocks, g.stat_w, ndyn, kmap, kdyn);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false>), dim3(g.p2_kblocks * padded),
                      dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
-                     g.p2_chunk, g.p2_chunks, g.p2_kblocks, g.stat_w);
+                     g.p2_chunk, g.p2_chunks, g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
   return hipGetLastError();
 }
 
@@ -466,6 +554,42 @@ hipError_t launch_pass2_mfma(const Geom& g, const float* X, const double* P,
   case D:                                                               \
     return v ? p2_launch<D, true>(g, X, P, bias, ln2, part, s)           \
              : p2_launch<D, false>(g, X, P, bias, ln2, part, s);
+    FGMM_P2(16) FGMM_P2(32) FGMM_P2(48) FGMM_P2(64) FGMM_P2(80) FGMM_P2(96)
+    FGMM_P2(112) FGMM_P2(128)
+#undef FGMM_P2
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_pass2_mfma_dyn(const Geom& g, const float* X, const double* P,
+                                 const double* bias, const double* ln2, double* part,
+                                 const int* ndyn, hipStream_t s) {
+  if (ndyn == nullptr) return hipErrorInvalidValue;
+  const bool v = x_is_vec(X, g.d);
+  switch (g.dp) {
+#define FGMM_P2(D)                                                       \
+  case D:                                                               \
+    return v ? p2_launch<D, true>(g, X, P, bias, ln2, part, s, ndyn)           \
+             : p2_launch<D, false>(g, X, P, bias, ln2, part, s, ndyn);
+    FGMM_P2(16) FGMM_P2(32) FGMM_P2(48) FGMM_P2(64) FGMM_P2(80) FGMM_P2(96)
+    FGMM_P2(112) FGMM_P2(128)
+#undef FGMM_P2
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_pass2_mfma_map(const Geom& g, const float* X, const double* P,
+                                 const double* bias, const double* ln2, double* part,
+                                 const int* kmap, const int* kdyn, hipStream_t s) {
+  if (kmap == nullptr || kdyn == nullptr) return hipErrorInvalidValue;
+  const bool v = x_is_vec(X, g.d);
+  switch (g.dp) {
+#define FGMM_P2(D)                                                       \
+  case D:                                                               \
+    return v ? p2_launch<D, true>(g, X, P, bias, ln2, part, s, nullptr, kmap, kdyn)           \
+             : p2_launch<D, false>(g, X, P, bias, ln2, part, s, nullptr, kmap, kdyn);
     FGMM_P2(16) FGMM_P2(32) FGMM_P2(48) FGMM_P2(64) FGMM_P2(80) FGMM_P2(96)
     FGMM_P2(112) FGMM_P2(128)
 #undef FGMM_P2

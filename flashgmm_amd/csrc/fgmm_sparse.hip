@@ -1,0 +1,581 @@
+// "sparse" variant: Pass 2 from the pair lists of Pass 1.
+//
+// The x32 Pass 1 of this variant lists, per point, every pair (n, k) it
+// evaluates exactly in fp64 (component, exact ll2): those whose fp32 upper
+// bound reaches within 40 bits of the point's best lower bound.  For the pairs
+// it leaves out it accumulates a per-component bound D_k on their total
+// responsibility (2^(upper bound - running max) each, summed over points in a
+// fixed order).  The statistics n_k, sum gamma x, sum gamma x^2 are sums over
+// the listed pairs only -- a few per point instead of K -- accumulated in
+// fp64, and the mass left out enters the error bounds
+//     eb = D_k + N 2^-126,  es = eb max|x|,  eq = eb max x^2.
+// The reduction flags components whose bounds could move mu, var or log pi by
+// more than a tenth of the parity bar (components whose responsibility lies
+// mostly outside the lists, i.e. starved ones); those are gathered and
+// recomputed over all points by the fp64 matrix-core Pass 2, as are the
+// points whose list outgrew its capacity.
+//
+// Kernels of one Pass 2 (all orders fixed, so results are reproducible):
+//   sp_sort_kernel    chunk of 1024 points: its entries (gamma formed here)
+//                     bitonic-sorted in LDS by (component, point); counts per
+//                     component
+//   sp_scan_*         exclusive scan of the counts in (component, chunk)
+//                     order: each component's entries become one contiguous
+//                     run ordered by point; overflow offsets; bound terms;
+//                     accumulation pieces of kSpPiece entries
+//   sp_place_kernel   moves each chunk's sorted entries to their place;
+//                     copies the overflow points out
+//   sp_piece_kernel   fp64 sums over one piece per workgroup
+//   sp_fold_kernel    per component, the sum of its pieces in order
+//   sp_flag_kernel    flagged components -> compact list and coefficients
+//
+// Reference kernel this replaces (file:line in the reference repository):
+//   Pass 2  flash_accumulate_stats_v2_kernel  flash_gmm/csrc/flash_gmm_cuda.cu:179-292
+#include <float.h>
+#include <limits.h>
+#include <math.h>
+
+#include "fgmm_internal.h"
+
+namespace fgmm {
+namespace {
+
+constexpr int kT = 256;            // threads of the chunk, scan-tile and piece kernels
+constexpr int kScanThreads = 1024;
+constexpr int kPointBits = 8;      // point index within a chunk in a sort key
+static_assert((1 << kPointBits) == kSpPts, "sort key layout");
+static_assert(kSpPts == kT, "one point per thread");
+constexpr int kAccUnroll = 4;      // entries per lane group in flight
+constexpr int kPieceGrid = 2048;   // workgroups of the piece kernel (grid-stride)
+
+// exclusive scan over the workgroup (NT threads), one value per thread
+template <int NT>
+__device__ inline int block_excl_scan(int v, int* sh, int* total) {
+  const int tid = threadIdx.x;
+  sh[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const int u = tid >= off ? sh[tid - off] : 0;
+    __syncthreads();
+    sh[tid] += u;
+    __syncthreads();
+  }
+  const int incl = sh[tid];
+  if (total != nullptr) *total = sh[NT - 1];
+  __syncthreads();
+  return incl - v;
+}
+
+// ---------------------------------------------------------------------------
+// per-chunk sort
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kT) void sp_sort_kernel(
+    long N, int Kp, int C, int nchunk, const int* __restrict__ pcnt, const int* __restrict__ pk,
+    const double* __restrict__ pv, const double* __restrict__ ln2, const float* __restrict__ xm,
+    int2* __restrict__ blk, int* __restrict__ ecnt, int* __restrict__ fcap,
+    int* __restrict__ cnt, int* __restrict__ ocnt, double* __restrict__ xsum) {
+  extern __shared__ int smem[];
+  int* keys = smem;                                              // [kSpChunkCap]
+  float* vals = reinterpret_cast<float*>(keys + kSpChunkCap);    // [kSpChunkCap]
+  int* hist = reinterpret_cast<int*>(vals + kSpChunkCap);        // [Kp]
+  __shared__ int sh[kT];
+  __shared__ int cut_sh, ov_sh, ek_sh;
+  __shared__ double r1[kT / 64];
+  const int ch = blockIdx.x, tid = threadIdx.x;
+  const long p0 = (long)ch * kSpPts;
+  for (int k = tid; k < Kp; k += kT) hist[k] = 0;
+  if (tid == 0) {
+    cut_sh = kSpPts;
+    ov_sh = 0;
+    ek_sh = 0;
+  }
+  // one point per thread
+  const long n = p0 + tid;
+  int m = 0, ov = 0;
+  double s1 = 0.0;
+  if (n < N) {
+    const int c = pcnt[n];
+    s1 = (double)xm[n];
+    if (c > C) ov = 1;
+    else m = c;
+  }
+  const int pos = block_excl_scan<kT>(m, sh, nullptr);
+  // entries of the kept points -> LDS keys (component, point) and gamma.
+  // Offsets come from the uncut prefix, so the points whose entries would
+  // pass the chunk capacity form a suffix of the chunk; they join the
+  // overflow points and the kept entries fill [0, Ek).
+  int mine = 0;
+  if (m > 0 && pos + m > kSpChunkCap) {
+    atomicMin(&cut_sh, tid);
+    ov = 1;
+  } else if (m > 0) {
+    const double l2 = ln2[n];
+    const int* kr = pk + (size_t)n * C;
+    const double* vr = pv + (size_t)n * C;
+    for (int i = 0; i < m; i++) {
+      const int k = kr[i];
+      keys[pos + i] = (k << kPointBits) | tid;
+      vals[pos + i] = exp2f((float)(vr[i] - l2));
+      atomicAdd(&hist[k], 1);   // integer counts: order-free
+    }
+    mine = m;
+  }
+  atomicAdd(&ov_sh, ov);
+  atomicAdd(&ek_sh, mine);
+  __syncthreads();
+  const int cut = cut_sh;
+  const int Ek = ek_sh;
+  int n2 = 2;
+  while (n2 < Ek) n2 <<= 1;
+  for (int i = Ek + tid; i < n2; i += kT) keys[i] = INT_MAX;
+  __syncthreads();
+  // bitonic sort of (keys, vals)
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < (n2 >> 1); i += kT) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const int a = keys[lo], b = keys[hi];
+        if ((a > b) == up) {
+          keys[lo] = b;
+          keys[hi] = a;
+          const float t = vals[lo];
+          vals[lo] = vals[hi];
+          vals[hi] = t;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  int2* out = blk + (size_t)ch * kSpChunkCap;
+  for (int i = tid; i < Ek; i += kT) out[i] = make_int2(keys[i], __float_as_int(vals[i]));
+  for (int k = tid; k < Kp; k += kT) cnt[(size_t)k * nchunk + ch] = hist[k];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s1 = fmax(s1, __shfl_xor(s1, off, 64));
+  if ((tid & 63) == 0) r1[tid >> 6] = s1;
+  __syncthreads();
+  if (tid == 0) {
+    double a = 0.0;
+    for (int w = 0; w < kT / 64; w++) a = fmax(a, r1[w]);
+    xsum[ch] = a;
+    ecnt[ch] = Ek;
+    fcap[ch] = cut;
+    ocnt[ch] = ov_sh;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// scan of the (component, chunk) counts: tile sums, scan of the tile sums,
+// tile rescans; then per-component runs and pieces
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kT) void sp_scan_tiles_kernel(long total, const int* __restrict__ cnt,
+                                                           int* __restrict__ tsum) {
+  __shared__ int red[kT / 64];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const long b0 = (long)t * kSpScanTile;
+  int s = 0;
+  for (int i = tid; i < kSpScanTile; i += kT) {
+    const long g = b0 + i;
+    if (g < total) s += cnt[g];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    int a = 0;
+    for (int w = 0; w < kT / 64; w++) a += red[w];
+    tsum[t] = a;
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void sp_scan_top_kernel(
+    long N, int Kp, int ntile, int nchunk, int* __restrict__ tsum, int* __restrict__ ocnt,
+    const double* __restrict__ xsum, int* __restrict__ seg, int* __restrict__ nov,
+    double* __restrict__ glob) {
+  __shared__ int sh[kScanThreads];
+  __shared__ double d1[kScanThreads / 64];
+  const int tid = threadIdx.x;
+  int carry = 0;
+  for (int b = 0; b < ntile; b += kScanThreads) {
+    const int i = b + tid;
+    const int v = i < ntile ? tsum[i] : 0;
+    int tot;
+    const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
+    if (i < ntile) tsum[i] = carry + ex;
+    carry += tot;
+  }
+  if (tid == 0) seg[Kp] = carry;
+  carry = 0;
+  for (int b = 0; b < nchunk; b += kScanThreads) {
+    const int i = b + tid;
+    const int v = i < nchunk ? ocnt[i] : 0;
+    int tot;
+    const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
+    if (i < nchunk) ocnt[i] = carry + ex;
+    carry += tot;
+  }
+  if (tid == 0) nov[0] = carry;
+  double a = 0.0;
+  for (int i = tid; i < nchunk; i += kScanThreads) a = fmax(a, xsum[i]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) a = fmax(a, __shfl_xor(a, off, 64));
+  if ((tid & 63) == 0) d1[tid >> 6] = a;
+  __syncthreads();
+  if (tid == 0) {
+    double xm2 = 0.0;
+    for (int w = 0; w < kScanThreads / 64; w++) xm2 = fmax(xm2, d1[w]);
+    glob[0] = (double)N * kSpFloor;
+    glob[1] = sqrt(xm2);
+    glob[2] = xm2;
+    glob[3] = 0.0;
+  }
+}
+
+// tile t: 16 consecutive counters per thread, rescanned with the tile offset
+__global__ __launch_bounds__(kT) void sp_scan_apply_kernel(long total, int* __restrict__ cnt,
+                                                           const int* __restrict__ tsum) {
+  constexpr int PER = kSpScanTile / kT;
+  __shared__ int sh[kT];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const long b0 = (long)t * kSpScanTile + (long)tid * PER;
+  int v[PER];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    v[i] = (b0 + i < total) ? cnt[b0 + i] : 0;
+    s += v[i];
+  }
+  int run = block_excl_scan<kT>(s, sh, nullptr) + tsum[t];
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    if (b0 + i < total) cnt[b0 + i] = run;
+    run += v[i];
+  }
+}
+
+// per component: start of its run, its pieces, the component of each piece
+__global__ __launch_bounds__(kScanThreads) void sp_runs_kernel(
+    int Kp, int nchunk, const int* __restrict__ cnt, int* __restrict__ seg,
+    int* __restrict__ pstart, int* __restrict__ pcomp, int* __restrict__ nov) {
+  __shared__ int sh[kScanThreads];
+  const int tid = threadIdx.x;
+  for (int k = tid; k < Kp; k += kScanThreads) seg[k] = cnt[(size_t)k * nchunk];
+  __syncthreads();   // seg[Kp] (the total) was written by the previous kernel
+  int carry = 0;
+  for (int b = 0; b < Kp; b += kScanThreads) {
+    const int k = b + tid;
+    int np = 0;
+    if (k < Kp) {
+      const int len = seg[k + 1] - seg[k];
+      np = (len + kSpPiece - 1) / kSpPiece;
+    }
+    int tot;
+    const int ex = block_excl_scan<kScanThreads>(np, sh, &tot);
+    if (k < Kp) {
+      pstart[k] = carry + ex;
+      for (int j = 0; j < np; j++) pcomp[carry + ex + j] = k;
+    }
+    carry += tot;
+  }
+  if (tid == 0) {
+    pstart[Kp] = carry;
+    nov[1] = carry;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// placement and overflow gather
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kT) void sp_place_kernel(
+    long N, int d, int Kp, int C, int nchunk, const int2* __restrict__ blk,
+    const int* __restrict__ ecnt, const int* __restrict__ fcap, const int* __restrict__ off,
+    const int* __restrict__ ooff, const int* __restrict__ pcnt, const float* __restrict__ X,
+    const double* __restrict__ ln2, int2* __restrict__ sorted, float* __restrict__ Xo,
+    double* __restrict__ ln2o) {
+  extern __shared__ int rs[];   // [Kp] first index of each component in the chunk
+  __shared__ int sh[kT];
+  __shared__ int ovn[kSpPts];   // overflow points of the chunk, in order
+  __shared__ int nov_sh;
+  const int ch = blockIdx.x, tid = threadIdx.x;
+  const long p0 = (long)ch * kSpPts;
+  const int E = ecnt[ch];
+  const int2* in = blk + (size_t)ch * kSpChunkCap;
+  for (int i = tid; i < E; i += kT) {
+    const int k = in[i].x >> kPointBits;
+    if (i == 0 || (in[i - 1].x >> kPointBits) != k) rs[k] = i;
+  }
+  __syncthreads();
+  for (int i = tid; i < E; i += kT) {
+    const int2 e = in[i];
+    const int k = e.x >> kPointBits;
+    const long n = p0 + (e.x & (kSpPts - 1));
+    sorted[(size_t)off[(size_t)k * nchunk + ch] + (i - rs[k])] = make_int2((int)n, e.y);
+  }
+  // overflow points: lists longer than C, or cut by the chunk capacity
+  const int cut = fcap[ch];
+  const long np = p0 + tid;
+  const int f = (np < N) && (pcnt[np] > C || (tid >= cut && pcnt[np] > 0)) ? 1 : 0;
+  int tot;
+  const int r = block_excl_scan<kT>(f, sh, &tot);
+  if (f) ovn[r] = tid;
+  if (tid == 0) nov_sh = tot;
+  __syncthreads();
+  const int nv = nov_sh;
+  if (nv == 0) return;
+  const long base = ooff[ch];
+  for (long idx = tid; idx < (long)nv * d; idx += kT) {
+    const int rr = (int)(idx / d), j = (int)(idx - (long)rr * d);
+    const long n = p0 + ovn[rr];
+    Xo[(size_t)(base + rr) * d + j] = X[(size_t)n * d + j];
+    if (j == 0) ln2o[base + rr] = ln2[n];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// piece sums: L lanes per entry (lane j holds features 4j..4j+3), H = 256/L
+// entries side by side, kAccUnroll entries per lane group loaded before use
+// ---------------------------------------------------------------------------
+template <int L, bool VEC>
+__global__ __launch_bounds__(kT) void sp_piece_kernel(
+    int d, int dp, int stat_w, const int* __restrict__ seg, const int* __restrict__ pstart,
+    const int* __restrict__ pcomp, const int* __restrict__ nov, const int2* __restrict__ sorted,
+    const float* __restrict__ X, double* __restrict__ prow) {
+  constexpr int H = kT / L;
+  __shared__ double sa[H][4 * L], sb[H][4 * L];
+  __shared__ double sn[H];
+  const int tid = threadIdx.x;
+  const int j = tid % L, h = tid / L;
+  const int j0 = 4 * j;
+  const int npiece = nov[1];
+  for (int pc = blockIdx.x; pc < npiece; pc += gridDim.x) {
+    const int k = pcomp[pc];
+    const int e0 = seg[k] + (pc - pstart[k]) * kSpPiece;
+    const int e1 = min(e0 + kSpPiece, seg[k + 1]);
+    double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
+    double nk = 0.0;
+    for (int e = e0 + h; e < e1; e += H * kAccUnroll) {
+      int2 en[kAccUnroll];
+      float4 xv[kAccUnroll];
+#pragma unroll
+      for (int u = 0; u < kAccUnroll; u++) {
+        const int eu = e + u * H;
+        en[u] = eu < e1 ? sorted[eu] : make_int2(0, 0);   // weight 0: no effect
+      }
+#pragma unroll
+      for (int u = 0; u < kAccUnroll; u++) {
+        xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j0 < d && en[u].y != 0) {
+          const float* src = X + (size_t)en[u].x * d + j0;
+          if (VEC) {
+            xv[u] = *reinterpret_cast<const float4*>(src);
+          } else {
+            xv[u].x = src[0];
+            if (j0 + 1 < d) xv[u].y = src[1];
+            if (j0 + 2 < d) xv[u].z = src[2];
+            if (j0 + 3 < d) xv[u].w = src[3];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kAccUnroll; u++) {
+        const double w = (double)__int_as_float(en[u].y);
+        const double x4[4] = {(double)xv[u].x, (double)xv[u].y, (double)xv[u].z,
+                              (double)xv[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const double wx = w * x4[q];   // exact: 24-bit times 24-bit
+          a[q] += wx;
+          b[q] = fma(wx, x4[q], b[q]);
+        }
+        nk += w;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      sa[h][j0 + q] = a[q];
+      sb[h][j0 + q] = b[q];
+    }
+    if (j == 0) sn[h] = nk;
+    __syncthreads();
+    double* row = prow + (size_t)pc * stat_w;
+    for (int f = tid; f < d; f += kT) {
+      double ta = 0.0, tb = 0.0;
+      for (int i = 0; i < H; i++) {
+        ta += sa[i][f];
+        tb += sb[i][f];
+      }
+      row[f] = ta;
+      row[dp + f] = tb;
+    }
+    if (tid == 0) {
+      double t = 0.0;
+      for (int i = 0; i < H; i++) t += sn[i];
+      row[2 * dp] = t;
+    }
+    __syncthreads();
+  }
+}
+
+// per component: its pieces summed in order, plus the bound columns
+__global__ __launch_bounds__(kT) void sp_fold_kernel(int d, int dp, int stat_w, int nblk,
+                                                     const int* __restrict__ pstart,
+                                                     const double* __restrict__ prow,
+                                                     const float* __restrict__ dmass,
+                                                     const double* __restrict__ glob,
+                                                     double* __restrict__ part_sp) {
+  __shared__ double red[kT / 64];
+  const int k = blockIdx.x, tid = threadIdx.x;
+  {   // D_k: the Pass-1 workgroups' bounds ([component][workgroup]), fixed order
+    double t = 0.0;
+    const float* dk = dmass + (size_t)k * nblk;
+    for (int b = tid; b < nblk; b += kT) t += (double)dk[b];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = t;
+  }
+  const int r0 = pstart[k], r1 = pstart[k + 1];
+  double* out = part_sp + (size_t)k * stat_w;
+  // columns [0, d) and [dp, dp + d) and 2dp: one per thread, rows in order
+  for (int f = tid; f < 2 * dp + 1; f += kT) {
+    if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
+    double a = 0.0;
+    int r = r0;
+    for (; r + 4 <= r1; r += 4) {
+      const double v0 = prow[(size_t)r * stat_w + f], v1 = prow[(size_t)(r + 1) * stat_w + f];
+      const double v2 = prow[(size_t)(r + 2) * stat_w + f], v3 = prow[(size_t)(r + 3) * stat_w + f];
+      a += v0;
+      a += v1;
+      a += v2;
+      a += v3;
+    }
+    for (; r < r1; r++) a += prow[(size_t)r * stat_w + f];
+    out[f] = a;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double t = 0.0;
+    for (int w = 0; w < kT / 64; w++) t += red[w];
+    const double eb = t * (1.0 + 0x1p-40) + glob[0];
+    out[2 * dp + 1] = eb;
+    out[2 * dp + 2] = eb * glob[1];
+    out[2 * dp + 3] = eb * glob[2];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// flagged components: compact list + gathered fp64 fragment coefficients
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kScanThreads) void sp_flag_kernel(
+    int K, int Kp, int dp, const int* __restrict__ flag, const double* __restrict__ P,
+    const double* __restrict__ bias, int* __restrict__ kmap, int* __restrict__ nflag,
+    double* __restrict__ Pf, double* __restrict__ biasf) {
+  __shared__ int sh[kScanThreads];
+  __shared__ int nf_sh;
+  const int tid = threadIdx.x;
+  int carry = 0;
+  for (int b = 0; b < Kp; b += kScanThreads) {
+    const int k = b + tid;
+    const int v = (k < K && flag[k] != 0) ? 1 : 0;
+    int tot;
+    const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
+    if (v) kmap[carry + ex] = k;
+    carry += tot;
+  }
+  if (tid == 0) nf_sh = carry;
+  __syncthreads();
+  const int nf = nf_sh;
+  const int n16 = (nf + 15) & ~15;
+  for (int i = nf + tid; i < n16; i += kScanThreads) kmap[i] = -1;
+  if (tid == 0) nflag[0] = nf;
+  __syncthreads();
+  // fragment layout: P[((ks * S1 + t) * 64 + 16 g + c] for component 16 ks + c
+  const int S1 = dp / 2;
+  const long per = (long)S1 * 4;
+  for (long idx = tid; idx < (long)n16 * per; idx += kScanThreads) {
+    const int i = (int)(idx / per);
+    const int r = (int)(idx - (long)i * per);
+    const int t = r >> 2, g = r & 3;
+    const int k = kmap[i];
+    const double v =
+        k >= 0 ? P[((size_t)(k >> 4) * S1 + t) * 64 + 16 * g + (k & 15)] : 0.0;
+    Pf[((size_t)(i >> 4) * S1 + t) * 64 + 16 * g + (i & 15)] = v;
+  }
+  for (int i = tid; i < n16; i += kScanThreads) {
+    const int k = kmap[i];
+    biasf[i] = k >= 0 ? bias[k] : -INFINITY;
+  }
+}
+
+template <int L>
+hipError_t piece_launch(const Geom& g, const float* X, const SpWs& sp, hipStream_t s) {
+  const long cap = sp_npiece_cap(g);
+  const int grid = (int)(cap < kPieceGrid ? cap : kPieceGrid);
+  if ((g.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0))
+    hipLaunchKernelGGL((sp_piece_kernel<L, true>), dim3(grid), dim3(kT), 0, s, g.d, g.dp,
+                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.prow);
+  else
+    hipLaunchKernelGGL((sp_piece_kernel<L, false>), dim3(grid), dim3(kT), 0, s, g.d, g.dp,
+                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.prow);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, const SpWs& sp,
+                               const double* ln2, hipStream_t s) {
+  if (g.variant != kSparse || g.dp > 128 || g.Kp > 8192 || g.stat_w < 2 * g.dp + 4 ||
+      g.sp_chunk != kSpPts || (long)g.sp_nchunk * kSpPts < g.N || w.pk == nullptr ||
+      w.pv == nullptr || w.pcnt == nullptr || w.dmass == nullptr || w.pC != g.sp_C ||
+      g.sp_C > kSpChunkCap)
+    return hipErrorInvalidValue;
+  const size_t lds_sort = (2 * (size_t)kSpChunkCap + (size_t)g.Kp) * sizeof(int);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)sp_sort_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)(2 * (size_t)kSpChunkCap + 8192) * (int)sizeof(int));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const long total = (long)g.Kp * g.sp_nchunk;
+  const int ntile = sp_ntile(g);
+  hipLaunchKernelGGL(sp_sort_kernel, dim3(g.sp_nchunk), dim3(kT), lds_sort, s, g.N, g.Kp,
+                     g.sp_C, g.sp_nchunk, w.pcnt, w.pk, w.pv, ln2, sp.xm, sp.blk, sp.ecnt,
+                     sp.fcap, sp.cnt, sp.ocnt, sp.xsum);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_scan_tiles_kernel, dim3(ntile), dim3(kT), 0, s, total, sp.cnt, sp.tsum);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_scan_top_kernel, dim3(1), dim3(kScanThreads), 0, s, g.N, g.Kp, ntile,
+                     g.sp_nchunk, sp.tsum, sp.ocnt, sp.xsum, sp.seg, sp.nov, sp.glob);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_scan_apply_kernel, dim3(ntile), dim3(kT), 0, s, total, sp.cnt, sp.tsum);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_runs_kernel, dim3(1), dim3(kScanThreads), 0, s, g.Kp, g.sp_nchunk,
+                     sp.cnt, sp.seg, sp.pstart, sp.pcomp, sp.nov);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_place_kernel, dim3(g.sp_nchunk), dim3(kT), sizeof(int) * (size_t)g.Kp,
+                     s, g.N, g.d, g.Kp, g.sp_C, g.sp_nchunk, sp.blk, sp.ecnt, sp.fcap, sp.cnt,
+                     sp.ocnt, w.pcnt, X, ln2, sp.sorted, sp.Xo, sp.ln2o);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (g.dp <= 16) e = piece_launch<4>(g, X, sp, s);
+  else if (g.dp <= 32) e = piece_launch<8>(g, X, sp, s);
+  else if (g.dp <= 64) e = piece_launch<16>(g, X, sp, s);
+  else e = piece_launch<32>(g, X, sp, s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_fold_kernel, dim3(g.K), dim3(kT), 0, s, g.d, g.dp, g.stat_w,
+                     g.p1_blocks, sp.pstart, sp.prow, w.dmass, sp.glob, sp.part_sp);
+  return hipGetLastError();
+}
+
+hipError_t launch_flag_compact(const Geom& g, const int* flag, const double* P,
+                               const double* bias, const SpWs& sp, hipStream_t s) {
+  if (g.variant != kSparse) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sp_flag_kernel, dim3(1), dim3(kScanThreads), 0, s, g.K, g.Kp, g.dp, flag,
+                     P, bias, sp.kmap, sp.nflag, sp.Pf, sp.biasf);
+  return hipGetLastError();
+}
+
+}  // namespace fgmm

@@ -59,6 +59,10 @@ constexpr float kWin = 40.0f;           // exact window, log2 units
 constexpr int kSlots = kX32Slots;       // slots per point (4 per lane group)
 static_assert(kSlots == 16, "Pass 1 writes 4 slots per lane group, Pass 2 reads 2 x uint4");
 constexpr unsigned short kNoSlot = 0xFFFF;
+constexpr int kX1Slots = 0, kX1Plain = 1, kX1Emit = 2;   // Pass-1 output modes
+// EMIT: pending pairs this far below the window are still evaluated exactly
+// (those further down have gamma < 2^-(kWin + kSpKeep) = 2^-126)
+constexpr float kSpKeep = 86.0f;
 
 __device__ inline f32x4 mfma32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -94,14 +98,17 @@ __device__ inline void load_quarter32(const float* __restrict__ X, long n, long 
 // [gQ, (g+1)Q) of point c.  Behind the two coefficient tiles LDS holds the
 // lanes' pending lists, entry i of thread t at i*512 + t (conflict-free).
 // ---------------------------------------------------------------------------
-template <int DP, bool VEC>
+template <int DP, bool VEC, int MODE>
 __global__ __launch_bounds__(512) void pass1_x32_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const float* __restrict__ P32,
     const float* __restrict__ bias32, const float* __restrict__ Z32,
     const double* __restrict__ V2, const double* __restrict__ b64,
     double* __restrict__ ln2, float* __restrict__ ln_out, double* __restrict__ lnsum,
     float* __restrict__ m32, float* __restrict__ xm, unsigned short* __restrict__ ck,
-    float* __restrict__ cg) {
+    float* __restrict__ cg, int* __restrict__ pk, double* __restrict__ pv,
+    int* __restrict__ pcnt, int pC, float* __restrict__ dmass) {
+  constexpr bool SLOTS = MODE == kX1Slots, EMIT = MODE == kX1Emit;
+  constexpr float kWinP1 = kWin;
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int TILE = kSub1 * S1 * 64;                 // floats per K tile
   constexpr int TV4 = TILE / 4;                         // float4 per tile
@@ -110,6 +117,7 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   extern __shared__ float smemf[];                      // [2][TILE], int2 [kPendL][512]
   __shared__ float sB[2][16 * kSub1], sZ[2][16 * kSub1];
   __shared__ double red[kW1];
+  __shared__ float dsh[2][kW1][16 * kSub1];   // EMIT: per-wave dropped-mass bounds of a tile
   int2* plist = reinterpret_cast<int2*>(smemf + 2 * TILE);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -161,6 +169,8 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   double eM = -INFINITY, eS = 0.0;        // exact online log-sum-exp (base 2)
   double sv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // largest exact pairs (slots)
   int sk4[4] = {-1, -1, -1, -1};
+  int pc = 0;                             // EMIT: entries of this point's list so far
+  const size_t pbase = (size_t)(valid ? n : 0) * pC;
   // Evaluates the pending pairs still inside the window and empties the
   // lists.  Wavefront-uniform.  The live entries of a point's four lanes
   // form one queue; round r evaluates every point's r-th entry: its four
@@ -173,7 +183,7 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
     int live_ = 0;                                                                    \
     for (int i_ = 0; i_ < npend; i_++) {                                              \
       const int2 e_ = plist[i_ * kThr1 + tid];                                        \
-      if (__int_as_float(e_.y) >= th_) {                                              \
+      if (__int_as_float(e_.y) >= (EMIT ? th_ - kSpKeep : th_)) {                     \
         plist[live_ * kThr1 + tid] = e_;                                              \
         live_++;                                                                      \
       }                                                                               \
@@ -210,17 +220,24 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
         const double mn_ = fmax(eM, v_);                                              \
         eS = eS * (double)exp2f((float)(eM - mn_)) + (double)exp2f((float)(v_ - mn_)); \
         eM = mn_;                                                                     \
-        double cv_ = v_;                                                              \
-        int ck_ = k_;                                                                 \
-        _Pragma("unroll") for (int q4_ = 0; q4_ < 4; q4_++) {                         \
-          if (cv_ > sv[q4_]) {                                                        \
-            const double tv_ = sv[q4_];                                               \
-            const int tk_ = sk4[q4_];                                                 \
-            sv[q4_] = cv_; sk4[q4_] = ck_; cv_ = tv_; ck_ = tk_;                      \
+        if (SLOTS) {                                                                  \
+          double cv_ = v_;                                                            \
+          int ck_ = k_;                                                               \
+          _Pragma("unroll") for (int q4_ = 0; q4_ < 4; q4_++) {                       \
+            if (cv_ > sv[q4_]) {                                                      \
+              const double tv_ = sv[q4_];                                             \
+              const int tk_ = sk4[q4_];                                               \
+              sv[q4_] = cv_; sk4[q4_] = ck_; cv_ = tv_; ck_ = tk_;                    \
+            }                                                                         \
           }                                                                           \
+        }                                                                             \
+        if (EMIT && pc + r_ < pC) {                                                   \
+          pk[pbase + pc + r_] = k_;                                                   \
+          pv[pbase + pc + r_] = v_;                                                   \
         }                                                                             \
       }                                                                               \
     }                                                                                 \
+    pc += tot_;                                                                       \
     npend = 0;                                                                        \
   }
 
@@ -262,10 +279,39 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
     lmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
     lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
     Mrun = fmaxf(Mrun, lmax);
-    const float thr = Mrun - kWin;
+    const float thr = Mrun - kWinP1;
     unsigned cm = 0;
 #pragma unroll
     for (int u = 0; u < 8; u++) cm |= (valid && hi[u] >= thr) ? (1u << u) : 0u;
+    if (EMIT) {
+      // the tile's pairs that never enter a list: gamma <= 2^(hi - Mrun); per
+      // component summed over the wavefront's 16 points (the 16 lanes of a
+      // lane group), then over the workgroup's waves in order
+      if (t > 0 && tid < 16 * kSub1) {   // previous tile's sums
+        float a = 0.f;
+#pragma unroll
+        for (int w = 0; w < kW1; w++) a += dsh[buf ^ 1][w][tid];
+        dmass[(size_t)((t - 1) * 16 * kSub1 + tid) * gridDim.x + blockIdx.x] = a * (1.0f + 0x1p-16f);
+      }
+      float dv[8];
+      bool any = false;
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        dv[u] = (valid && !(cm & (1u << u))) ? exp2f(hi[u] - Mrun) : 0.f;
+        any = any || dv[u] > 0.f;
+      }
+      if (__ballot(any) != 0ull) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) dv[u] += __shfl_xor(dv[u], o, 64);
+        }
+      }
+      if (c == 0) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) dsh[buf][wave][(u >> 2) * 16 + 4 * g + (u & 3)] = dv[u];
+      }
+    }
     if (__ballot(cm != 0) != 0ull) {
       if (__ballot(npend + __popc(cm) > kPendL) != 0ull) FGMM_X1_FLUSH(thr)
 #pragma unroll
@@ -282,7 +328,13 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   }
 #undef FGMM_X1_GLOAD
 #undef FGMM_X1_LSTORE
-  FGMM_X1_FLUSH(Mrun - kWin)
+  if (EMIT && tid < 16 * kSub1) {   // last tile's sums
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < kW1; w++) a += dsh[(ntiles - 1) & 1][w][tid];
+    dmass[(size_t)((ntiles - 1) * 16 * kSub1 + tid) * gridDim.x + blockIdx.x] = a * (1.0f + 0x1p-16f);
+  }
+  FGMM_X1_FLUSH(Mrun - kWinP1)
 #undef FGMM_X1_FLUSH
 
   // merge the exact sums of the four lane groups of each point
@@ -299,7 +351,7 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   const double l2 = eM + log2(eS);
   const double lnat = l2 * kLn2;
   if (valid) {
-    if (ck != nullptr) {   // the slots and window data feed the x32 Pass 2 only
+    if (SLOTS) {   // the slots and window data feed the x32 Pass 2 only
       const size_t base = (size_t)n * kSlots + 4 * g;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -310,6 +362,10 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
         m32[n] = Mrun;
         xm[n] = xmax2;
       }
+    }
+    if (EMIT && g == 0) {
+      pcnt[n] = pc;
+      xm[n] = xmax2;
     }
     if (g == 0) {
       ln2[n] = l2;
@@ -690,22 +746,37 @@ __global__ __launch_bounds__(256) void x32_fix_kernel(
   }
 }
 
-template <int DP, bool VEC>
-hipError_t x1_launch(const Geom& g, const float* X, const X32Ws& w, double* ln2,
-                     float* ln_out, double* lnsum, hipStream_t s) {
+template <int DP, bool VEC, int MODE>
+hipError_t x1_launch_mode(const Geom& g, const float* X, const X32Ws& w, double* ln2,
+                          float* ln_out, double* lnsum, hipStream_t s) {
   constexpr size_t lds = 2 * (size_t)kSub1 * (DP / 2) * 64 * sizeof(float) +
                          (size_t)kPendL * kThr1 * sizeof(int2);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)pass1_x32_kernel<DP, VEC>,
+    hipError_t e = hipFuncSetAttribute((const void*)pass1_x32_kernel<DP, VEC, MODE>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((pass1_x32_kernel<DP, VEC>), dim3(g.p1_blocks), dim3(kThr1), lds, s, X,
-                     g.N, g.d, g.Kp, w.P32, w.bias32, w.Z32, w.V, w.b64, ln2, ln_out, lnsum,
-                     w.m32, w.xm, w.ck, w.cg);
+  hipLaunchKernelGGL((pass1_x32_kernel<DP, VEC, MODE>), dim3(g.p1_blocks), dim3(kThr1), lds, s,
+                     X, g.N, g.d, g.Kp, w.P32, w.bias32, w.Z32, w.V, w.b64, ln2, ln_out, lnsum,
+                     w.m32, w.xm, w.ck, w.cg, w.pk, w.pv, w.pcnt, w.pC, w.dmass);
   return hipGetLastError();
+}
+
+// slots for the x32 Pass 2; pair lists for the sparse Pass 2; else the
+// log-normalizer alone
+template <int DP, bool VEC>
+hipError_t x1_launch(const Geom& g, const float* X, const X32Ws& w, double* ln2,
+                     float* ln_out, double* lnsum, hipStream_t s) {
+  if (w.ck != nullptr) return x1_launch_mode<DP, VEC, kX1Slots>(g, X, w, ln2, ln_out, lnsum, s);
+  if (w.pk != nullptr) {
+    if (w.pv == nullptr || w.pcnt == nullptr || w.xm == nullptr || w.dmass == nullptr ||
+        w.pC < 1)
+      return hipErrorInvalidValue;
+    return x1_launch_mode<DP, VEC, kX1Emit>(g, X, w, ln2, ln_out, lnsum, s);
+  }
+  return x1_launch_mode<DP, VEC, kX1Plain>(g, X, w, ln2, ln_out, lnsum, s);
 }
 
 template <int DP, bool VEC>

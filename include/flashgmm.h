@@ -26,8 +26,10 @@
  * variant: FGMM_VARIANT_AUTO picks a kernel family from a table keyed by
  * (K, d); FGMM_VARIANT_VALU (fp64 vector ALU), FGMM_VARIANT_MFMA (fp64
  * matrix-core distance), FGMM_VARIANT_X32 (fp32 matrix-core distance with
- * the significant pairs recomputed in fp64) or FGMM_VARIANT_MIXED (the x32
- * log-normalizer pass with the fp64 statistics pass) force one.
+ * the significant pairs recomputed in fp64), FGMM_VARIANT_MIXED (the x32
+ * log-normalizer pass with the fp64 statistics pass) or FGMM_VARIANT_SPARSE
+ * (the x32 log-normalizer pass listing each point's significant pairs, and a
+ * statistics pass over those lists) force one.
  */
 #ifndef FLASHGMM_H
 #define FLASHGMM_H
@@ -48,6 +50,7 @@ extern "C" {
 #define FGMM_VARIANT_MFMA 2
 #define FGMM_VARIANT_X32 3   /* fp32 matrix-core distance + exact fp64 refinement */
 #define FGMM_VARIANT_MIXED 4 /* x32 Pass 1 (exact log-normalizer) + fp64 MFMA Pass 2 */
+#define FGMM_VARIANT_SPARSE 5 /* x32 Pass 1 + statistics from the listed exact pairs */
 
 /* Library ABI version (major*100 + minor). */
 int fgmm_version(void);
@@ -127,7 +130,8 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0,
  * Gamma-returning E-step on the flash schedule: Pass 1 (log-normalizer), then
  * a second sweep that recomputes every (n, k) log-density and writes
  * gamma[N][K] = exp(ll - log_normalizer).  No other N x K array is formed.
- * Workspace: fgmm_workspace_bytes.  FGMM_VARIANT_X32 runs as MFMA here.
+ * Workspace: fgmm_workspace_bytes.  FGMM_VARIANT_X32, _MIXED and _SPARSE run
+ * as MFMA here.
  * Replaces flash_e_step (flash_gmm/csrc/binding.cpp:51-60,97-99), which the
  * reference implements on the CPU only (flash_gmm_cpu.cpp:108-168) and
  * refuses for CUDA tensors.
@@ -144,7 +148,7 @@ size_t fgmm_standard_e_step_workspace_bytes(long N, int K, int d, int variant);
  * Standard (materialising) E-step: the log-density matrix L[N][K] is written
  * to the workspace in fp64, then a row log-sum-exp writes
  * log_normalizer[N] and gamma[N][K] = exp(L - log_normalizer).
- * FGMM_VARIANT_X32 runs as MFMA here.
+ * FGMM_VARIANT_X32, _MIXED and _SPARSE run as MFMA here.
  * Replaces standard_e_step_cuda = standard_e_step_kernel +
  * logsumexp_normalize_kernel (flash_gmm/csrc/flash_gmm_cuda.cu:328-400),
  * bound as standard_e_step (flash_gmm/csrc/binding.cpp:35-49,95-96).
@@ -185,7 +189,8 @@ int fgmm_standard_m_step(const float* X, const float* gamma, long N, int K, int 
  *                      (nullable, device double) = mean log-normalizer.
  * All calls of one iteration use the same workspace (of
  * fgmm_stream_workspace_bytes(chunk_rows, ...)), chunk_rows and variant, in
- * stream order.  FGMM_VARIANT_X32 runs as MFMA here.
+ * stream order.  FGMM_VARIANT_X32 runs as MFMA and FGMM_VARIANT_SPARSE as
+ * MIXED here.
  * Replaces the streaming iteration of StreamingFlashGMM / StreamingFlashGMMAsync
  * .em_step (flash_gmm/flash_gmm_v9.py:145-326), which makes one pass over
  * the chunks per stage; here each chunk is read once per iteration.

@@ -58,8 +58,8 @@ def test_version_and_variant_table(lib):
 
 def test_workspace_bytes(lib):
     for N, K, d in ((4096, 8, 32), (65536, 256, 128), (1048576, 512, 128), (1, 1, 1), (5, 3, 256)):
-        for v in (0, 1, 2, 4):
-            if v in (2, 4) and d > 128:
+        for v in (0, 1, 2, 4, 5):
+            if v in (2, 4, 5) and d > 128:
                 assert lib.fgmm_workspace_bytes(N, K, d, v) == 0
                 continue
             b = lib.fgmm_workspace_bytes(N, K, d, v)
@@ -118,6 +118,8 @@ def test_argument_errors_before_device_work(lib):
     assert _em(lib, d=200, variant=2) == 1 and b"MFMA" in lib.fgmm_last_error()
     assert _em(lib, variant=7) == 1 and b"variant" in lib.fgmm_last_error()
     assert _em(lib, d=200, variant=4) == 1 and b"mixed" in lib.fgmm_last_error()
+    assert _em(lib, d=200, variant=5) == 1 and b"sparse" in lib.fgmm_last_error()
+    assert _em(lib, K=8193, variant=5) == 1 and b"sparse" in lib.fgmm_last_error()
     for i in range(8):
         assert _em(lib, null=i) == 1 and b"must not be NULL" in lib.fgmm_last_error()
     assert _em(lib, ws=None) == 2 and b"NULL" in lib.fgmm_last_error()

@@ -26,7 +26,7 @@ CASES = [(1, None), (2, None), (3, None), (4, None), (5, 131072)]
 def variants_for(K, d):
     v = ["valu"]
     if d <= 128:
-        v += ["mfma", "x32", "mixed"]
+        v += ["mfma", "x32", "mixed", "sparse"]
     return v
 
 
@@ -76,7 +76,7 @@ def test_golden_vectors(cuda, name):
     with np.load(path, allow_pickle=False) as z:
         g = {k: z[k] for k in z.files}
     t = to_dev(cuda, g["X"], g["mu"], g["var"], g["log_pi"])
-    for variant in ("valu", "mfma", "x32", "mixed"):
+    for variant in ("valu", "mfma", "x32", "mixed", "sparse"):
         print(f"[case] golden {name} variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], g["ln"], f"{name} {variant}")
@@ -227,7 +227,7 @@ def test_unaligned_and_noncontiguous_inputs(cuda):
     Xu = big[1:].view(X.shape)                    # 4-byte offset: scalar load path
     assert Xu.data_ptr() % 16 != 0
     t = to_dev(cuda, mu, var, lp)
-    for variant in ("valu", "mfma", "x32", "mixed"):
+    for variant in ("valu", "mfma", "x32", "mixed", "sparse"):
         print(f"[case] unaligned X variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(Xu, *t, variant=variant)]
         check_params(out[:3], ref[:3], f"unaligned {variant}")
@@ -284,7 +284,7 @@ def test_x32_starved_component_takes_exact_path(cuda):
     ref = O.c_m_step_update(n_k, s_k, sq_k, N)
     assert 1e-9 < n_k[4] < 1e-8, n_k[4]      # starved, at the clamp
     t = to_dev(cuda, X, mu, var, lp)
-    for variant in ("x32", "mixed", "mfma"):
+    for variant in ("x32", "mixed", "sparse", "mfma"):
         print(f"[case] starved component variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], ln, f"starved {variant}")
@@ -304,8 +304,36 @@ def test_x32_crowded_window_overflows_slots(cuda):
     lp = np.full(K, -np.log(K), np.float32)
     ref = O.c_em_fused(X, mu, var, lp)
     t = to_dev(cuda, X, mu, var, lp)
-    for variant in ("x32", "mixed", "mfma"):
+    for variant in ("x32", "mixed", "sparse", "mfma"):
         print(f"[case] crowded window variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], ref[3], f"crowded {variant}")
         check_params(out[:3], ref[:3], f"crowded {variant}")
+
+
+def test_sparse_partial_overflow_and_repeatability(cuda):
+    """40 nearly identical components around the origin and 8 separated ones:
+    points near the origin list ~40 pairs, more than the 32 entries a point
+    may list, and take the dense fp64 pass; the others take the listed pairs.
+    Both kinds of rows meet in the reduction.  Two calls agree bit for bit."""
+    import torch
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(11)
+    K, d = 48, 32
+    far = rng.uniform(-30, 30, (8, d))
+    Xa = rng.normal(0, 1, (3000, d))
+    Xb = far[rng.integers(0, 8, 5000)] + rng.normal(0, 1, (5000, d))
+    X = np.concatenate([Xa, Xb])[rng.permutation(8000)].astype(np.float32)
+    mu = np.concatenate([rng.normal(0, 0.02, (40, d)), far]).astype(np.float32)
+    var = rng.uniform(0.9, 1.1, (K, d)).astype(np.float32)
+    lp = np.full(K, -np.log(K), np.float32)
+    ref = O.c_em_fused(X, mu, var, lp)
+    t = to_dev(cuda, X, mu, var, lp)
+    print("[case] sparse partial overflow", flush=True)
+    a = C.flash_em_fused(*t, variant="sparse")
+    out = [o.cpu().numpy() for o in a]
+    check_ln(out[3], ref[3], "sparse partial overflow")
+    check_params(out[:3], ref[:3], "sparse partial overflow")
+    b = C.flash_em_fused(*t, variant="sparse")
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

@@ -57,7 +57,8 @@ def test_streamed_ragged_small_and_x32_request(cuda):
     lp = np.log(rng.dirichlet(np.ones(K))).astype(np.float32)
     ref = O.c_em_fused(X, mu, var, lp)
     p = to_dev(cuda, mu, var, lp)
-    for chunk, variant in ((700, None), (64, "valu"), (1000, "x32"), (333, "mixed")):
+    for chunk, variant in ((700, None), (64, "valu"), (1000, "x32"), (333, "mixed"),
+                           (500, "sparse")):
         print(f"[case] ragged stream chunk={chunk} variant={variant}", flush=True)
         out = streaming.StreamingFlashGMMAsync(chunk_size=chunk, variant=variant).em_step(
             torch.from_numpy(X), *p)
