@@ -76,6 +76,10 @@ Geom make_geom(long N, int K, int d, int variant) {
   long tiles = (N + tile - 1) / tile;
   long S = (512 + g.p2_kblocks - 1) / g.p2_kblocks;
   if (S < (N + 16383) / 16384) S = (N + 16383) / 16384;
+  // sparse: the dense passes run over the flagged components (often one
+  // 16-component subtile) and the overflow points; 512 chunks keep the GPU
+  // busy for those (their partial rows are written for those rows only)
+  if (g.variant == kSparse && S < 512) S = 512;
   if (S > tiles) S = tiles;
   if (S < 1) S = 1;
   long chunk = round_up_l((N + S - 1) / S, tile);
@@ -107,13 +111,13 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   char* ecnt = take(sizeof(int) * nch);
   char* fcap = take(sizeof(int) * nch);
   char* cnt = take(sizeof(int) * Kp * nch);
-  char* tsum = take(sizeof(int) * (size_t)sp_ntile(g));
+  char* rowtot = take(sizeof(int) * Kp);
   char* ocnt = take(sizeof(int) * nch);
   char* xsum = take(sizeof(double) * nch);
   char* seg = take(sizeof(int) * (Kp + 1));
   char* pstart = take(sizeof(int) * (Kp + 1));
   char* pcomp = take(sizeof(int) * npc);
-  char* nov = take(sizeof(int) * 2);
+  char* nov = take(sizeof(int) * 3);
   char* glob = take(sizeof(double) * 4);
   char* sorted = take(sizeof(int2) * NC);
   char* prow = take(sizeof(double) * npc * (size_t)g.stat_w);
@@ -139,7 +143,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
     sp->ecnt = reinterpret_cast<int*>(ecnt);
     sp->fcap = reinterpret_cast<int*>(fcap);
     sp->cnt = reinterpret_cast<int*>(cnt);
-    sp->tsum = reinterpret_cast<int*>(tsum);
+    sp->rowtot = reinterpret_cast<int*>(rowtot);
     sp->ocnt = reinterpret_cast<int*>(ocnt);
     sp->xsum = reinterpret_cast<double*>(xsum);
     sp->seg = reinterpret_cast<int*>(seg);
@@ -245,6 +249,9 @@ static int validate_shape(long N, int K, int d, int variant) {
   if (variant == kSparse && (d > 128 || K > 8192))
     return fail(FGMM_EINVAL, "the sparse variant supports d <= 128 and K <= 8192 (got d=%d, K=%d)",
                 d, K);
+  if (variant == kSparse && N * (long)(K < kSpCap ? K : kSpCap) > 2147483647L)
+    return fail(FGMM_EINVAL, "the sparse variant needs N * min(K, %d) < 2^31 (got N=%ld)", kSpCap,
+                N);
   if (variant == kMixed && d > 128)
     return fail(FGMM_EINVAL, "the mixed variant supports d <= 128 (got %d)", d);
   if (variant == kMfma && d > 128)

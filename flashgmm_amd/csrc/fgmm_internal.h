@@ -102,14 +102,15 @@ constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
 // Sparse variant.  Pass 1 lists every pair it evaluates exactly (those whose
 // fp32 upper bound reaches within 40 bits of the point's best lower bound, and
 // pending pairs down to 126 bits below it) and bounds, per component, the
-// responsibility of the pairs it leaves out: sum of 2^(upper bound - running
-// max) over them, plus 2^-126 per point for pairs below that.
+// responsibility of the pairs that never became pending: 2^(upper bound -
+// running max) each.  Each remaining pair -- pending ones dropped further
+// down, listed ones whose responsibility comes out below 2^-126 -- has gamma
+// < 2^-126; one such pair per (point, component) at most.
 constexpr double kSpFloor = 0x1p-126;
 constexpr int kSpCap = 32;            // list entries per point (at most K)
 constexpr int kSpPts = 256;           // points per sort chunk
 constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
-constexpr int kSpPiece = 256;         // entries per accumulation piece
-constexpr int kSpScanTile = 4096;     // counters per scan tile
+constexpr int kSpPiece = 64;          // entries per accumulation piece (at least)
 
 // Buffers of the sparse Pass 2 (see fgmm_sparse.hip).
 struct SpWs {
@@ -117,15 +118,16 @@ struct SpWs {
   int2* blk;           // [nchunk][kSpChunkCap] chunk entries sorted by (component, point)
   int* ecnt;           // [nchunk] entries of the chunk
   int* fcap;           // [nchunk] first point of the chunk cut by the chunk capacity
-  int* cnt;            // [Kp][nchunk] entries per (component, chunk) -> offsets
-  int* tsum;           // [ntile] scan tile sums -> offsets
+  int* cnt;            // [Kp][nchunk] entries per (component, chunk) -> offsets within
+                       // the component's run
+  int* rowtot;         // [Kp] entries per component
   int* ocnt;           // [nchunk] overflow points per chunk -> offsets
   double* xsum;        // [nchunk] max xm over the chunk
   int* seg;            // [Kp + 1] start of each component's entries
   int* pstart;         // [Kp + 1] first accumulation piece of each component
   int* pcomp;          // [npiece_cap] component of each piece
-  int* nov;            // [2] overflow points, pieces
-  double* glob;        // [4] N 2^-126, max_n max_j |x_nj|, its square
+  int* nov;            // [3] overflow points, pieces, entries per piece
+  double* glob;        // [4] N 2^-126 (with margin), max_n max_j |x_nj|, its square
   int2* sorted;        // [N * C] (point, float gamma bits) by (component, point)
   double* prow;        // [npiece_cap][stat_w] piece sums
   float* Xo;           // [N][d] rows of the overflow points
@@ -136,12 +138,10 @@ struct SpWs {
   double* Pf;          // fp64 fragment coefficients of the flagged components
   double* biasf;       // [Kp]
 };
-inline int sp_ntile(const Geom& g) {
-  return (int)(((long)g.Kp * g.sp_nchunk + kSpScanTile - 1) / kSpScanTile);
-}
-inline long sp_npiece_cap(const Geom& g) {
-  return (long)g.N * g.sp_C / kSpPiece + g.Kp + 1;
-}
+// Piece rows: a fixed budget; the device widens the pieces past kSpPiece
+// entries when the lists hold more than kSpPiece x budget entries.
+inline long sp_piece_budget(const Geom& g) { return g.N / 64 > 4096 ? g.N / 64 : 4096; }
+inline long sp_npiece_cap(const Geom& g) { return sp_piece_budget(g) + g.Kp + 1; }
 
 // Error model of the fp32 expanded distance (x32 variant).  ll32 is
 // fl(a0 + a1) with a0 = sum_j P1_kj x_j^2 and a1 = bias_k + sum_j P2_kj x_j

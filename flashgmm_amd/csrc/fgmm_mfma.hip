@@ -222,7 +222,9 @@ __global__ __launch_bounds__(512) void pass1_mfma_kernel(
 // SPLIT: the four wavefronts share one 16-component subtile and take one
 // 16-point quarter of each tile each (for few components, e.g. the flagged
 // ones of the sparse variant); their sums are combined in a fixed order.
-template <int DP, bool VEC, bool SPLIT>
+// PERSIST: the grid strides over the items (device-counted work); otherwise
+// workgroup w processes item w.
+template <int DP, bool VEC, bool SPLIT, bool PERSIST>
 __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const double* __restrict__ P,
     const double* __restrict__ bias, const double* __restrict__ ln2,
@@ -235,24 +237,29 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
   __shared__ float xs[2][kP2Tile * XS];
   __shared__ double ls[2][kP2Tile];
 
-  // XCD-aware decode of the linear workgroup id
-  const int w = blockIdx.x;
-  const int xcd = w & 7, local = w >> 3;
+  // Work items are (component block, point chunk) pairs.  With device counts
+  // (ndyn: rows, kdyn: compacted components) only the blocks and chunks that
+  // hold work are enumerated and the grid strides over them; otherwise the
+  // grid has one workgroup per item.
+  if (ndyn != nullptr) {
+    const long nd = *ndyn;
+    N = nd < N ? nd : N;
+    nchunks = (int)((N + chunk - 1) / chunk);
+  }
+  int kact = Kp;   // compacted components: the first round_up(*kdyn, 16) slots
+  if (kdyn != nullptr) {
+    kact = (*kdyn + 15) & ~15;
+    const int per = (SPLIT ? 1 : kP2Waves) * 16;
+    kblocks = (kact + per - 1) / per;
+  }
+  const int nitems = kblocks * ((nchunks + 7) / 8 * 8);
+  auto body = [&](const int item) {   // one item; its returns end the item
+  // XCD-aware decode of the item: items w and w+8 run on the same XCD, so the
+  // blocks that read the same point chunk share that XCD's L2
+  const int xcd = item & 7, local = item >> 3;
   const int kb = local % kblocks;
   const int chunk_id = (local / kblocks) * 8 + xcd;
   if (chunk_id >= nchunks) return;
-  if (ndyn != nullptr) {   // rows past the device count: no chunk, no partial row
-    const long nd = *ndyn;
-    N = nd < N ? nd : N;
-    if ((long)chunk_id * chunk >= N) return;
-  }
-
-  // compacted components (kdyn): only the first round_up(*kdyn, 16) slots
-  int kact = Kp;
-  if (kdyn != nullptr) {
-    kact = (*kdyn + 15) & ~15;
-    if (kb * (SPLIT ? 1 : kP2Waves) * 16 >= kact) return;
-  }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -462,6 +469,12 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     double* o = row(c);
     if (o != nullptr) o[2 * DP] = nk;
   }
+  };
+  if (PERSIST) {
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) body(item);
+  } else if ((int)blockIdx.x < nitems) {
+    body(blockIdx.x);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -506,16 +519,26 @@ static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
                             hipStream_t s, const int* ndyn = nullptr,
                             const int* kmap = nullptr, const int* kdyn = nullptr) {
   const int padded = (g.p2_chunks + 7) / 8 * 8;
-  if (kmap != nullptr) {   // compacted components: one 16-component subtile per workgroup
-    const int kblocks = g.Kp / 16;
-    hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, true>), dim3(kblocks * padded),
+  // device-counted work: a grid of at most kPersist workgroups strides over it
+  constexpr int kPersist = 1024;
+  if (kmap != nullptr) {   // compacted components: one 16-component subtile per item
+    const int items = g.Kp / 16 * padded;
+    hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, true, true>), dim3(items < kPersist ? items : kPersist),
                        dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
-                       g.p2_chunk, g.p2_chunks, kblocks, g.stat_w, ndyn, kmap, kdyn);
+                       g.p2_chunk, g.p2_chunks, g.Kp / 16, g.stat_w, ndyn, kmap, kdyn);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false>), dim3(g.p2_kblocks * padded),
-                     dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
-                     g.p2_chunk, g.p2_chunks, g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
+  const int items = g.p2_kblocks * padded;
+  if (ndyn != nullptr) {
+    hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false, true>),
+                       dim3(items < kPersist ? items : kPersist), dim3(64 * kP2Waves), 0, s, X,
+                       g.N, g.d, g.Kp, P, bias, ln2, part, g.p2_chunk, g.p2_chunks,
+                       g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false, false>), dim3(items), dim3(64 * kP2Waves),
+                     0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part, g.p2_chunk, g.p2_chunks,
+                     g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
   return hipGetLastError();
 }
 

@@ -2,12 +2,14 @@
 //
 // The x32 Pass 1 of this variant lists, per point, every pair (n, k) it
 // evaluates exactly in fp64 (component, exact ll2): those whose fp32 upper
-// bound reaches within 40 bits of the point's best lower bound.  For the pairs
-// it leaves out it accumulates a per-component bound D_k on their total
-// responsibility (2^(upper bound - running max) each, summed over points in a
-// fixed order).  The statistics n_k, sum gamma x, sum gamma x^2 are sums over
-// the listed pairs only -- a few per point instead of K -- accumulated in
-// fp64, and the mass left out enters the error bounds
+// bound reaches within 40 bits of the point's best lower bound (and pending
+// pairs down to 126 bits below it).  For the pairs that never became pending
+// it accumulates a per-component bound D_k on their total responsibility
+// (2^(upper bound - running max) each, summed over points in a fixed order);
+// every other pair left out has gamma < 2^-126.  The statistics n_k,
+// sum gamma x, sum gamma x^2 are sums over the listed pairs only -- a few per
+// point instead of K -- accumulated in fp64, and the mass left out enters the
+// error bounds
 //     eb = D_k + N 2^-126,  es = eb max|x|,  eq = eb max x^2.
 // The reduction flags components whose bounds could move mu, var or log pi by
 // more than a tenth of the parity bar (components whose responsibility lies
@@ -16,13 +18,13 @@
 // points whose list outgrew its capacity.
 //
 // Kernels of one Pass 2 (all orders fixed, so results are reproducible):
-//   sp_sort_kernel    chunk of 1024 points: its entries (gamma formed here)
+//   sp_sort_kernel    chunk of 256 points: its entries (gamma formed here)
 //                     bitonic-sorted in LDS by (component, point); counts per
 //                     component
-//   sp_scan_*         exclusive scan of the counts in (component, chunk)
-//                     order: each component's entries become one contiguous
-//                     run ordered by point; overflow offsets; bound terms;
-//                     accumulation pieces of kSpPiece entries
+//   sp_rowscan_kernel per component, exclusive scan of its chunk counts
+//   sp_top_kernel     runs (each component's entries become one contiguous
+//                     run ordered by point), accumulation pieces of >= 64
+//                     entries, overflow offsets, bound terms
 //   sp_place_kernel   moves each chunk's sorted entries to their place;
 //                     copies the overflow points out
 //   sp_piece_kernel   fp64 sums over one piece per workgroup
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
   float* vals = reinterpret_cast<float*>(keys + kSpChunkCap);    // [kSpChunkCap]
   int* hist = reinterpret_cast<int*>(vals + kSpChunkCap);        // [Kp]
   __shared__ int sh[kT];
-  __shared__ int cut_sh, ov_sh, ek_sh;
+  __shared__ int cut_sh, ov_sh, ek_sh, ep_sh;
   __shared__ double r1[kT / 64];
   const int ch = blockIdx.x, tid = threadIdx.x;
   const long p0 = (long)ch * kSpPts;
@@ -88,6 +90,7 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     cut_sh = kSpPts;
     ov_sh = 0;
     ek_sh = 0;
+    ep_sh = 0;
   }
   // one point per thread
   const long n = p0 + tid;
@@ -114,20 +117,27 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     const double* vr = pv + (size_t)n * C;
     for (int i = 0; i < m; i++) {
       const int k = kr[i];
-      keys[pos + i] = (k << kPointBits) | tid;
-      vals[pos + i] = exp2f((float)(vr[i] - l2));
-      atomicAdd(&hist[k], 1);   // integer counts: order-free
+      const float gam = exp2f((float)(vr[i] - l2));
+      // below 2^-126 the pair joins the per-(point, component) floor
+      const bool keep = gam >= 0x1p-126f;
+      keys[pos + i] = keep ? (k << kPointBits) | tid : INT_MAX;
+      vals[pos + i] = gam;
+      if (keep) {
+        atomicAdd(&hist[k], 1);   // integer counts: order-free
+        mine++;
+      }
     }
-    mine = m;
+    atomicMax(&ep_sh, pos + m);
   }
   atomicAdd(&ov_sh, ov);
   atomicAdd(&ek_sh, mine);
   __syncthreads();
   const int cut = cut_sh;
-  const int Ek = ek_sh;
+  const int Ek = ek_sh;    // kept entries; after the sort they lead
+  const int Ep = ep_sh;    // positions written
   int n2 = 2;
-  while (n2 < Ek) n2 <<= 1;
-  for (int i = Ek + tid; i < n2; i += kT) keys[i] = INT_MAX;
+  while (n2 < Ep) n2 <<= 1;
+  for (int i = Ep + tid; i < n2; i += kT) keys[i] = INT_MAX;
   __syncthreads();
   // bitonic sort of (keys, vals)
   for (int size = 2; size <= n2; size <<= 1) {
@@ -166,47 +176,84 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scan of the (component, chunk) counts: tile sums, scan of the tile sums,
-// tile rescans; then per-component runs and pieces
+// scans: each component's chunk counts (one wavefront per component) ->
+// offsets within its run; then the runs, pieces and overflow offsets
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kT) void sp_scan_tiles_kernel(long total, const int* __restrict__ cnt,
-                                                           int* __restrict__ tsum) {
-  __shared__ int red[kT / 64];
-  const int t = blockIdx.x, tid = threadIdx.x;
-  const long b0 = (long)t * kSpScanTile;
-  int s = 0;
-  for (int i = tid; i < kSpScanTile; i += kT) {
-    const long g = b0 + i;
-    if (g < total) s += cnt[g];
-  }
+__global__ __launch_bounds__(kT) void sp_rowscan_kernel(int Kp, int nchunk, int* __restrict__ cnt,
+                                                        int* __restrict__ rowtot) {
+  const int lane = threadIdx.x & 63;
+  const int k = blockIdx.x * (kT / 64) + (threadIdx.x >> 6);
+  if (k >= Kp) return;
+  int* row = cnt + (size_t)k * nchunk;
+  int carry = 0;
+  for (int b = 0; b < nchunk; b += 64) {
+    const int i = b + lane;
+    const int v = i < nchunk ? row[i] : 0;
+    int x = v;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-  if ((tid & 63) == 0) red[tid >> 6] = s;
-  __syncthreads();
-  if (tid == 0) {
-    int a = 0;
-    for (int w = 0; w < kT / 64; w++) a += red[w];
-    tsum[t] = a;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int u = __shfl_up(x, off, 64);
+      if (lane >= off) x += u;
+    }
+    if (i < nchunk) row[i] = carry + x - v;
+    carry += __shfl(x, 63, 64);
   }
+  if (lane == 0) rowtot[k] = carry;
 }
 
-__global__ __launch_bounds__(kScanThreads) void sp_scan_top_kernel(
-    long N, int Kp, int ntile, int nchunk, int* __restrict__ tsum, int* __restrict__ ocnt,
-    const double* __restrict__ xsum, int* __restrict__ seg, int* __restrict__ nov,
-    double* __restrict__ glob) {
+__global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
+    long N, int Kp, int nchunk, long budget, const int* __restrict__ rowtot, int* __restrict__ ocnt,
+    const double* __restrict__ xsum, int* __restrict__ seg, int* __restrict__ pstart,
+    int* __restrict__ pcomp, int* __restrict__ nov, double* __restrict__ glob) {
   __shared__ int sh[kScanThreads];
   __shared__ double d1[kScanThreads / 64];
+  extern __shared__ int ps[];   // [Kp + 1] first piece of each component
   const int tid = threadIdx.x;
   int carry = 0;
-  for (int b = 0; b < ntile; b += kScanThreads) {
-    const int i = b + tid;
-    const int v = i < ntile ? tsum[i] : 0;
+  for (int b = 0; b < Kp; b += kScanThreads) {
+    const int k = b + tid;
+    const int len = k < Kp ? rowtot[k] : 0;
     int tot;
-    const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
-    if (i < ntile) tsum[i] = carry + ex;
+    const int ex = block_excl_scan<kScanThreads>(len, sh, &tot);
+    if (k < Kp) seg[k] = carry + ex;
     carry += tot;
   }
-  if (tid == 0) seg[Kp] = carry;
+  // piece length: kSpPiece, or more when the piece rows would pass the budget
+  // (pieces <= total / piece + Kp <= budget + Kp)
+  const long total = carry;
+  int piece = kSpPiece;
+  if ((total + piece - 1) / piece > budget) piece = (int)((total + budget - 1) / budget);
+  int pcarry = 0;
+  for (int b = 0; b < Kp; b += kScanThreads) {
+    const int k = b + tid;
+    const int len = k < Kp ? rowtot[k] : 0;
+    const int np = (len + piece - 1) / piece;
+    int ptot;
+    const int pex = block_excl_scan<kScanThreads>(np, sh, &ptot);
+    if (k < Kp) {
+      pstart[k] = pcarry + pex;
+      ps[k] = pcarry + pex;
+    }
+    pcarry += ptot;
+  }
+  if (tid == 0) {
+    seg[Kp] = carry;
+    pstart[Kp] = pcarry;
+    ps[Kp] = pcarry;
+    nov[1] = pcarry;
+    nov[2] = piece;
+  }
+  __syncthreads();
+  // component of each piece: the last k with ps[k] <= piece index
+  for (int pc = tid; pc < pcarry; pc += kScanThreads) {
+    int lo = 0, hi = Kp;   // ps[lo] <= pc < ps[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (ps[mid] <= pc) lo = mid;
+      else hi = mid;
+    }
+    pcomp[pc] = lo;
+  }
   carry = 0;
   for (int b = 0; b < nchunk; b += kScanThreads) {
     const int i = b + tid;
@@ -226,62 +273,10 @@ __global__ __launch_bounds__(kScanThreads) void sp_scan_top_kernel(
   if (tid == 0) {
     double xm2 = 0.0;
     for (int w = 0; w < kScanThreads / 64; w++) xm2 = fmax(xm2, d1[w]);
-    glob[0] = (double)N * kSpFloor;
+    glob[0] = (double)N * kSpFloor * (1.0 + 0x1p-10);
     glob[1] = sqrt(xm2);
     glob[2] = xm2;
     glob[3] = 0.0;
-  }
-}
-
-// tile t: 16 consecutive counters per thread, rescanned with the tile offset
-__global__ __launch_bounds__(kT) void sp_scan_apply_kernel(long total, int* __restrict__ cnt,
-                                                           const int* __restrict__ tsum) {
-  constexpr int PER = kSpScanTile / kT;
-  __shared__ int sh[kT];
-  const int t = blockIdx.x, tid = threadIdx.x;
-  const long b0 = (long)t * kSpScanTile + (long)tid * PER;
-  int v[PER];
-  int s = 0;
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    v[i] = (b0 + i < total) ? cnt[b0 + i] : 0;
-    s += v[i];
-  }
-  int run = block_excl_scan<kT>(s, sh, nullptr) + tsum[t];
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    if (b0 + i < total) cnt[b0 + i] = run;
-    run += v[i];
-  }
-}
-
-// per component: start of its run, its pieces, the component of each piece
-__global__ __launch_bounds__(kScanThreads) void sp_runs_kernel(
-    int Kp, int nchunk, const int* __restrict__ cnt, int* __restrict__ seg,
-    int* __restrict__ pstart, int* __restrict__ pcomp, int* __restrict__ nov) {
-  __shared__ int sh[kScanThreads];
-  const int tid = threadIdx.x;
-  for (int k = tid; k < Kp; k += kScanThreads) seg[k] = cnt[(size_t)k * nchunk];
-  __syncthreads();   // seg[Kp] (the total) was written by the previous kernel
-  int carry = 0;
-  for (int b = 0; b < Kp; b += kScanThreads) {
-    const int k = b + tid;
-    int np = 0;
-    if (k < Kp) {
-      const int len = seg[k + 1] - seg[k];
-      np = (len + kSpPiece - 1) / kSpPiece;
-    }
-    int tot;
-    const int ex = block_excl_scan<kScanThreads>(np, sh, &tot);
-    if (k < Kp) {
-      pstart[k] = carry + ex;
-      for (int j = 0; j < np; j++) pcomp[carry + ex + j] = k;
-    }
-    carry += tot;
-  }
-  if (tid == 0) {
-    pstart[Kp] = carry;
-    nov[1] = carry;
   }
 }
 
@@ -290,7 +285,8 @@ __global__ __launch_bounds__(kScanThreads) void sp_runs_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kT) void sp_place_kernel(
     long N, int d, int Kp, int C, int nchunk, const int2* __restrict__ blk,
-    const int* __restrict__ ecnt, const int* __restrict__ fcap, const int* __restrict__ off,
+    const int* __restrict__ ecnt, const int* __restrict__ fcap, const int* __restrict__ seg,
+    const int* __restrict__ off,
     const int* __restrict__ ooff, const int* __restrict__ pcnt, const float* __restrict__ X,
     const double* __restrict__ ln2, int2* __restrict__ sorted, float* __restrict__ Xo,
     double* __restrict__ ln2o) {
@@ -311,7 +307,7 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
     const int2 e = in[i];
     const int k = e.x >> kPointBits;
     const long n = p0 + (e.x & (kSpPts - 1));
-    sorted[(size_t)off[(size_t)k * nchunk + ch] + (i - rs[k])] = make_int2((int)n, e.y);
+    sorted[(size_t)seg[k] + off[(size_t)k * nchunk + ch] + (i - rs[k])] = make_int2((int)n, e.y);
   }
   // overflow points: lists longer than C, or cut by the chunk capacity
   const int cut = fcap[ch];
@@ -348,11 +344,11 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
   const int tid = threadIdx.x;
   const int j = tid % L, h = tid / L;
   const int j0 = 4 * j;
-  const int npiece = nov[1];
+  const int npiece = nov[1], piece = nov[2];
   for (int pc = blockIdx.x; pc < npiece; pc += gridDim.x) {
     const int k = pcomp[pc];
-    const int e0 = seg[k] + (pc - pstart[k]) * kSpPiece;
-    const int e1 = min(e0 + kSpPiece, seg[k + 1]);
+    const int e0 = seg[k] + (pc - pstart[k]) * piece;
+    const int e1 = min(e0 + piece, seg[k + 1]);
     double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
     double nk = 0.0;
     for (int e = e0 + h; e < e1; e += H * kAccUnroll) {
@@ -442,13 +438,12 @@ __global__ __launch_bounds__(kT) void sp_fold_kernel(int d, int dp, int stat_w, 
     if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
     double a = 0.0;
     int r = r0;
-    for (; r + 4 <= r1; r += 4) {
-      const double v0 = prow[(size_t)r * stat_w + f], v1 = prow[(size_t)(r + 1) * stat_w + f];
-      const double v2 = prow[(size_t)(r + 2) * stat_w + f], v3 = prow[(size_t)(r + 3) * stat_w + f];
-      a += v0;
-      a += v1;
-      a += v2;
-      a += v3;
+    for (; r + 8 <= r1; r += 8) {
+      double v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) v[q] = prow[(size_t)(r + q) * stat_w + f];
+#pragma unroll
+      for (int q = 0; q < 8; q++) a += v[q];
     }
     for (; r < r1; r++) a += prow[(size_t)r * stat_w + f];
     out[f] = a;
@@ -539,26 +534,21 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const long total = (long)g.Kp * g.sp_nchunk;
-  const int ntile = sp_ntile(g);
   hipLaunchKernelGGL(sp_sort_kernel, dim3(g.sp_nchunk), dim3(kT), lds_sort, s, g.N, g.Kp,
                      g.sp_C, g.sp_nchunk, w.pcnt, w.pk, w.pv, ln2, sp.xm, sp.blk, sp.ecnt,
                      sp.fcap, sp.cnt, sp.ocnt, sp.xsum);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_scan_tiles_kernel, dim3(ntile), dim3(kT), 0, s, total, sp.cnt, sp.tsum);
+  hipLaunchKernelGGL(sp_rowscan_kernel, dim3((g.Kp + kT / 64 - 1) / (kT / 64)), dim3(kT), 0, s,
+                     g.Kp, g.sp_nchunk, sp.cnt, sp.rowtot);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_scan_top_kernel, dim3(1), dim3(kScanThreads), 0, s, g.N, g.Kp, ntile,
-                     g.sp_nchunk, sp.tsum, sp.ocnt, sp.xsum, sp.seg, sp.nov, sp.glob);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_scan_apply_kernel, dim3(ntile), dim3(kT), 0, s, total, sp.cnt, sp.tsum);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_runs_kernel, dim3(1), dim3(kScanThreads), 0, s, g.Kp, g.sp_nchunk,
-                     sp.cnt, sp.seg, sp.pstart, sp.pcomp, sp.nov);
+  hipLaunchKernelGGL(sp_top_kernel, dim3(1), dim3(kScanThreads), sizeof(int) * (g.Kp + 1), s,
+                     g.N, g.Kp, g.sp_nchunk,
+                     sp_piece_budget(g), sp.rowtot, sp.ocnt, sp.xsum, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.glob);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(sp_place_kernel, dim3(g.sp_nchunk), dim3(kT), sizeof(int) * (size_t)g.Kp,
-                     s, g.N, g.d, g.Kp, g.sp_C, g.sp_nchunk, sp.blk, sp.ecnt, sp.fcap, sp.cnt,
-                     sp.ocnt, w.pcnt, X, ln2, sp.sorted, sp.Xo, sp.ln2o);
+                     s, g.N, g.d, g.Kp, g.sp_C, g.sp_nchunk, sp.blk, sp.ecnt, sp.fcap, sp.seg,
+                     sp.cnt, sp.ocnt, w.pcnt, X, ln2, sp.sorted, sp.Xo, sp.ln2o);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (g.dp <= 16) e = piece_launch<4>(g, X, sp, s);
   else if (g.dp <= 32) e = piece_launch<8>(g, X, sp, s);
