@@ -91,8 +91,8 @@ struct X32Ws {
   float* cg;           // [N][kX32Slots] slot responsibilities (exact)
   int* flag;           // [Kp] components whose statistics are recomputed exactly
   // sparse variant: per-point pair lists written by Pass 1
-  int* pk;             // [N][pC] component
-  double* pv;          // [N][pC] exact ll2
+  int* pk;             // [N][pC] component (| kSpBound for a bound entry)
+  double* pv;          // [N][pC] exact ll2 (bound entry: upper bound of ll2)
   int* pcnt;           // [N] entries of the point (> pC: the list overflowed)
   int pC;
   float* dmass;        // [Kp][p1_blocks] bound on the unlisted responsibility mass
@@ -100,13 +100,15 @@ struct X32Ws {
 constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
 
 // Sparse variant.  Pass 1 lists every pair it evaluates exactly (those whose
-// fp32 upper bound reaches within 40 bits of the point's best lower bound, and
-// pending pairs down to 126 bits below it) and bounds, per component, the
-// responsibility of the pairs that never became pending: 2^(upper bound -
-// running max) each.  Each remaining pair -- pending ones dropped further
-// down, listed ones whose responsibility comes out below 2^-126 -- has gamma
-// < 2^-126; one such pair per (point, component) at most.
+// fp32 upper bound reaches within 40 bits of the point's best lower bound);
+// pending pairs the rising maximum pushed out of that window, down to 126
+// bits below it, are listed as bound entries (component | kSpBound, fp32
+// upper bound of ll2).  For the pairs that never became pending it bounds the
+// total responsibility per component: 2^(upper bound - running max) each.
+// Each remaining pair has gamma < 2^-126; one such pair per (point,
+// component) at most.
 constexpr double kSpFloor = 0x1p-126;
+constexpr int kSpBound = 0x40000000;
 constexpr int kSpCap = 32;            // list entries per point (at most K)
 constexpr int kSpPts = 256;           // points per sort chunk
 constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
@@ -115,7 +117,8 @@ constexpr int kSpPiece = 64;          // entries per accumulation piece (at leas
 // Buffers of the sparse Pass 2 (see fgmm_sparse.hip).
 struct SpWs {
   float* xm;           // [N] max_j x_nj^2 (Pass 1)
-  int2* blk;           // [nchunk][kSpChunkCap] chunk entries sorted by (component, point)
+  int2* blk;           // [nchunk][kSpChunkCap] chunk entries sorted by (component, point);
+                       // gamma < 0 marks a bound entry (its bound, negated)
   int* ecnt;           // [nchunk] entries of the chunk
   int* fcap;           // [nchunk] first point of the chunk cut by the chunk capacity
   int* cnt;            // [Kp][nchunk] entries per (component, chunk) -> offsets within

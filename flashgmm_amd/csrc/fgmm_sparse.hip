@@ -116,12 +116,14 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     const int* kr = pk + (size_t)n * C;
     const double* vr = pv + (size_t)n * C;
     for (int i = 0; i < m; i++) {
-      const int k = kr[i];
-      const float gam = exp2f((float)(vr[i] - l2));
+      const int kb = kr[i];
+      const int k = kb & (kSpBound - 1);
+      float gam = exp2f((float)(vr[i] - l2));
+      if (kb & kSpBound) gam *= 1.0f + 0x1p-20f;   // stays an upper bound
       // below 2^-126 the pair joins the per-(point, component) floor
       const bool keep = gam >= 0x1p-126f;
       keys[pos + i] = keep ? (k << kPointBits) | tid : INT_MAX;
-      vals[pos + i] = gam;
+      vals[pos + i] = (kb & kSpBound) ? -gam : gam;
       if (keep) {
         atomicAdd(&hist[k], 1);   // integer counts: order-free
         mine++;
@@ -337,10 +339,10 @@ template <int L, bool VEC>
 __global__ __launch_bounds__(kT) void sp_piece_kernel(
     int d, int dp, int stat_w, const int* __restrict__ seg, const int* __restrict__ pstart,
     const int* __restrict__ pcomp, const int* __restrict__ nov, const int2* __restrict__ sorted,
-    const float* __restrict__ X, double* __restrict__ prow) {
+    const float* __restrict__ X, const float* __restrict__ xm, double* __restrict__ prow) {
   constexpr int H = kT / L;
   __shared__ double sa[H][4 * L], sb[H][4 * L];
-  __shared__ double sn[H];
+  __shared__ double sn[H][4];
   const int tid = threadIdx.x;
   const int j = tid % L, h = tid / L;
   const int j0 = 4 * j;
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
     const int e0 = seg[k] + (pc - pstart[k]) * piece;
     const int e1 = min(e0 + piece, seg[k + 1]);
     double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
-    double nk = 0.0;
+    double nk = 0.0, eb = 0.0, es = 0.0, eq = 0.0;
     for (int e = e0 + h; e < e1; e += H * kAccUnroll) {
       int2 en[kAccUnroll];
       float4 xv[kAccUnroll];
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
 #pragma unroll
       for (int u = 0; u < kAccUnroll; u++) {
         xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j0 < d && en[u].y != 0) {
+        if (j0 < d && __int_as_float(en[u].y) > 0.f) {
           const float* src = X + (size_t)en[u].x * d + j0;
           if (VEC) {
             xv[u] = *reinterpret_cast<const float4*>(src);
@@ -377,6 +379,15 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
 #pragma unroll
       for (int u = 0; u < kAccUnroll; u++) {
         const double w = (double)__int_as_float(en[u].y);
+        if (w < 0.0) {   // bound entry: error columns only
+          if (j == 0) {
+            const double x2 = (double)xm[en[u].x];
+            eb -= w;
+            es -= w * sqrt(x2);
+            eq -= w * x2;
+          }
+          continue;
+        }
         const double x4[4] = {(double)xv[u].x, (double)xv[u].y, (double)xv[u].z,
                               (double)xv[u].w};
 #pragma unroll
@@ -393,7 +404,12 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
       sa[h][j0 + q] = a[q];
       sb[h][j0 + q] = b[q];
     }
-    if (j == 0) sn[h] = nk;
+    if (j == 0) {
+      sn[h][0] = nk;
+      sn[h][1] = eb;
+      sn[h][2] = es;
+      sn[h][3] = eq;
+    }
     __syncthreads();
     double* row = prow + (size_t)pc * stat_w;
     for (int f = tid; f < d; f += kT) {
@@ -405,10 +421,10 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
       row[f] = ta;
       row[dp + f] = tb;
     }
-    if (tid == 0) {
+    if (tid < 4) {
       double t = 0.0;
-      for (int i = 0; i < H; i++) t += sn[i];
-      row[2 * dp] = t;
+      for (int i = 0; i < H; i++) t += sn[i][tid];
+      row[2 * dp + tid] = t;
     }
     __syncthreads();
   }
@@ -422,6 +438,7 @@ __global__ __launch_bounds__(kT) void sp_fold_kernel(int d, int dp, int stat_w, 
                                                      const double* __restrict__ glob,
                                                      double* __restrict__ part_sp) {
   __shared__ double red[kT / 64];
+  __shared__ double fsh[3];
   const int k = blockIdx.x, tid = threadIdx.x;
   {   // D_k: the Pass-1 workgroups' bounds ([component][workgroup]), fixed order
     double t = 0.0;
@@ -433,8 +450,8 @@ __global__ __launch_bounds__(kT) void sp_fold_kernel(int d, int dp, int stat_w, 
   }
   const int r0 = pstart[k], r1 = pstart[k + 1];
   double* out = part_sp + (size_t)k * stat_w;
-  // columns [0, d) and [dp, dp + d) and 2dp: one per thread, rows in order
-  for (int f = tid; f < 2 * dp + 1; f += kT) {
+  // columns [0, d), [dp, dp + d), 2dp .. 2dp+3: one per thread, rows in order
+  for (int f = tid; f < 2 * dp + 4; f += kT) {
     if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
     double a = 0.0;
     int r = r0;
@@ -446,16 +463,19 @@ __global__ __launch_bounds__(kT) void sp_fold_kernel(int d, int dp, int stat_w, 
       for (int q = 0; q < 8; q++) a += v[q];
     }
     for (; r < r1; r++) a += prow[(size_t)r * stat_w + f];
-    out[f] = a;
+    if (f <= 2 * dp) out[f] = a;
+    else fsh[f - 2 * dp - 1] = a;
   }
   __syncthreads();
   if (tid == 0) {
+    // bound entries (their own max|x|) + pairs that never became pending
+    // (the global max) + the floor
     double t = 0.0;
     for (int w = 0; w < kT / 64; w++) t += red[w];
-    const double eb = t * (1.0 + 0x1p-40) + glob[0];
-    out[2 * dp + 1] = eb;
-    out[2 * dp + 2] = eb * glob[1];
-    out[2 * dp + 3] = eb * glob[2];
+    const double dk = t * (1.0 + 0x1p-40) + glob[0];
+    out[2 * dp + 1] = fsh[0] + dk;
+    out[2 * dp + 2] = fsh[1] + dk * glob[1];
+    out[2 * dp + 3] = fsh[2] + dk * glob[2];
   }
 }
 
@@ -509,10 +529,10 @@ hipError_t piece_launch(const Geom& g, const float* X, const SpWs& sp, hipStream
   const int grid = (int)(cap < kPieceGrid ? cap : kPieceGrid);
   if ((g.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0))
     hipLaunchKernelGGL((sp_piece_kernel<L, true>), dim3(grid), dim3(kT), 0, s, g.d, g.dp,
-                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.prow);
+                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.xm, sp.prow);
   else
     hipLaunchKernelGGL((sp_piece_kernel<L, false>), dim3(grid), dim3(kT), 0, s, g.d, g.dp,
-                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.prow);
+                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.xm, sp.prow);
   return hipGetLastError();
 }
 

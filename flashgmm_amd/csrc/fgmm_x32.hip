@@ -60,9 +60,20 @@ constexpr int kSlots = kX32Slots;       // slots per point (4 per lane group)
 static_assert(kSlots == 16, "Pass 1 writes 4 slots per lane group, Pass 2 reads 2 x uint4");
 constexpr unsigned short kNoSlot = 0xFFFF;
 constexpr int kX1Slots = 0, kX1Plain = 1, kX1Emit = 2;   // Pass-1 output modes
-// EMIT: pending pairs this far below the window are still evaluated exactly
-// (those further down have gamma < 2^-(kWin + kSpKeep) = 2^-126)
+// EMIT: pending pairs that end up less than this far below the window are
+// listed as bound entries (those further down have gamma < 2^-(kWin +
+// kSpKeep) = 2^-126)
 constexpr float kSpKeep = 86.0f;
+
+// Sum over the 16 lanes of each DPP row (lanes 16g .. 16g+15); every lane of
+// the row gets the sum.  Quad swaps, then half-row and row mirrors.
+__device__ inline float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return v;
+}
 
 __device__ inline f32x4 mfma32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -181,11 +192,37 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   {                                                                                   \
     const float th_ = (thr_);                                                         \
     int live_ = 0;                                                                    \
-    for (int i_ = 0; i_ < npend; i_++) {                                              \
-      const int2 e_ = plist[i_ * kThr1 + tid];                                        \
-      if (__int_as_float(e_.y) >= (EMIT ? th_ - kSpKeep : th_)) {                     \
-        plist[live_ * kThr1 + tid] = e_;                                              \
-        live_++;                                                                      \
+    if (EMIT) {   /* left the window by < kSpKeep bits: listed as bound entries */    \
+      int nb_ = 0;                                                                    \
+      for (int i_ = 0; i_ < npend; i_++) {                                            \
+        const float h_ = __int_as_float(plist[i_ * kThr1 + tid].y);                   \
+        nb_ += (h_ < th_ && h_ >= th_ - kSpKeep) ? 1 : 0;                             \
+      }                                                                               \
+      const int b0_ = __shfl(nb_, c, 64), b1_ = __shfl(nb_, 16 + c, 64);              \
+      const int b2_ = __shfl(nb_, 32 + c, 64), b3_ = __shfl(nb_, 48 + c, 64);         \
+      int bp_ = pc + (g > 0 ? b0_ : 0) + (g > 1 ? b1_ : 0) + (g > 2 ? b2_ : 0);       \
+      pc += b0_ + b1_ + b2_ + b3_;                                                    \
+      for (int i_ = 0; i_ < npend; i_++) {                                            \
+        const int2 e_ = plist[i_ * kThr1 + tid];                                      \
+        const float h_ = __int_as_float(e_.y);                                        \
+        if (h_ >= th_) {                                                              \
+          plist[live_ * kThr1 + tid] = e_;                                            \
+          live_++;                                                                    \
+        } else if (h_ >= th_ - kSpKeep) {                                             \
+          if (bp_ < pC) {                                                             \
+            pk[pbase + bp_] = e_.x | kSpBound;                                        \
+            pv[pbase + bp_] = (double)h_;                                             \
+          }                                                                           \
+          bp_++;                                                                      \
+        }                                                                             \
+      }                                                                               \
+    } else {                                                                          \
+      for (int i_ = 0; i_ < npend; i_++) {                                            \
+        const int2 e_ = plist[i_ * kThr1 + tid];                                      \
+        if (__int_as_float(e_.y) >= th_) {                                            \
+          plist[live_ * kThr1 + tid] = e_;                                            \
+          live_++;                                                                    \
+        }                                                                             \
       }                                                                               \
     }                                                                                 \
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");                            \
@@ -302,10 +339,7 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
       }
       if (__ballot(any) != 0ull) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) dv[u] += __shfl_xor(dv[u], o, 64);
-        }
+        for (int u = 0; u < 8; u++) dv[u] = row16_sum(dv[u]);
       }
       if (c == 0) {
 #pragma unroll
