@@ -1,15 +1,15 @@
 """Benchmark: fused Flash-GMM EM iterations per second on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--config 2] [--all]
-                    [--variant auto|valu|mfma] [--no-cpu-baseline]
+                    [--variant auto|valu|mfma|x32|mixed|sparse] [--no-cpu-baseline]
 
 A step is one fused EM iteration (precompute -> Pass 1 -> Pass 2 ->
 reduction/M-step) over the configuration's full synthetic data set, which is
 resident in HBM before timing starts.  The timed region runs ``steps``
 iterations back to back on the device (parameters fed forward on the device,
 no host synchronisation inside), bracketed by ``torch.cuda.synchronize()``.
-Pass 2's launch durations are measured live with HIP events on the launch
-stream (``fgmm_profile_*``) and give the roofline figure.
+Each pass's launch durations are measured live with HIP events on the launch
+stream (``fgmm_profile_*``); the dominant kernel's give the roofline figure.
 
 Default workload: configuration 2 (N=65536, K=256, d=128, fp32), the metric's
 headline shape.  ``--all`` adds one JSON line per configuration after the
@@ -72,16 +72,46 @@ def copy_probe(mib: int) -> None:
     del src, dst
 
 
-def pass2_flops(cfg) -> float:
-    # gamma recompute (4 flops per (n,k,j)) + gamma^T [X, X^2] (4 per (n,k,j))
-    return 8.0 * cfg.N * cfg.K * cfg.d
-
-
 def pass2_peak() -> float:
     # Pass 2's 8 flops per (n,k,j) run at different precisions: the distance
     # recompute (4) and sum gamma*x^2 (2) on fp64 matrix cores, sum gamma*x (2)
     # on fp32 matrix cores.  The binding peak is the time-weighted mix.
     return 8.0 / (6.0 / FP64_PEAK + 2.0 / FP32_PEAK)
+
+
+FP32_SWEEP = ("x32", "mixed", "sparse")   # Pass 1 on fp32 matrix cores
+
+
+def dominant_roofline(cfg, variant, kernels):
+    """Roofline of the kernel that takes the most time per iteration.
+
+    Pass 1 is a dense sweep over all (n, k): 4 flops per (n, k, j) (the
+    x^2 and x contractions), on fp32 matrix cores for the x32-based variants
+    and on fp64 matrix cores (fp64 VALU for valu) otherwise.  The dense Pass 2
+    recomputes the distance and accumulates gamma^T [X, X^2]: 8 flops per
+    (n, k, j) at its fp64/fp32 instruction mix.  The sparse variant's Pass 2
+    touches only the listed pairs and is not dominant."""
+    nkd = float(cfg.N) * cfg.K * cfg.d
+    t1 = kernels["pass1"]["ms_avg"] / 1e3
+    t2 = kernels["pass2"]["ms_avg"] / 1e3
+    if variant == "sparse" or t1 >= t2:
+        peak = FP32_PEAK if variant in FP32_SWEEP else FP64_PEAK
+        flops, t = 4.0 * nkd, t1
+        out = {"kernel": "pass1 (log-normalizer sweep, "
+                         + ("fp32 matrix cores" if variant in FP32_SWEEP else "fp64") + ")",
+               "peak": peak / 1e12}
+    else:
+        flops, t = 8.0 * nkd, t2
+        peak = FP32_PEAK
+        out = {"kernel": "pass2 (gamma recompute + sufficient statistics)",
+               "peak": peak / 1e12,
+               "peak_at_kernel_precision": pass2_peak() / 1e12}
+    achieved = flops / t if t > 0 else 0.0
+    out.update({"bound": "mfma", "achieved": achieved / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / peak, "flops_per_launch": flops})
+    if "peak_at_kernel_precision" in out:
+        out["frac_at_kernel_precision"] = achieved / pass2_peak()
+    return out
 
 
 def run_gpu(cid, steps, warmup, variant):
@@ -202,17 +232,19 @@ def cpu_baseline(cid, budget_s):
                       f"{per*1000:.1f} ms each"}
 
 
-def measured_traffic(cid):
-    """HBM bytes per Pass-2 launch from the committed rocprofv3 counter runs
-    (profiles/hbm_traffic.json), or None when that workload was not profiled."""
+def measured_traffic(cid, variant, kernel):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 counter runs (profiles/hbm_traffic.json), or None when that
+    workload, variant and kernel were not profiled."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         rec = json.load(open(path)).get(f"C{cid}")
     except (OSError, ValueError):
         return None
-    if not rec:
+    if not rec or rec.get("variant") != variant:
         return None
-    return rec["read_bytes"] + rec["write_bytes"]
+    r = rec.get(kernel.split(" ")[0])
+    return None if r is None else r["read_bytes"] + r["write_bytes"]
 
 
 def line_for(cid, args, with_cpu):
@@ -220,10 +252,11 @@ def line_for(cid, args, with_cpu):
     r = run_gpu(cid, args.steps, args.warmup, args.variant)
     sec = r["elapsed"]
     its = args.steps / sec
-    p2 = r["kernels"]["pass2"]["ms_avg"] / 1e3
     F_total = cfg.flops_per_iter()
     roof_t = max(F_total / FP32_PEAK, cfg.bytes_per_iter() / HBM_PEAK)
-    achieved = pass2_flops(cfg) / p2 if p2 > 0 else 0.0
+    roof = dominant_roofline(cfg, r["variant"], r["kernels"])
+    roof["traffic"] = measured_traffic(cid, r["variant"], roof["kernel"])
+    roof["traffic_unit"] = "HBM bytes/launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE, profiles/)"
     out = {
         "metric": "EM iters/s (N=65536,K=256,d=128 fp32) + % of HBM / fp32-MFMA roofline",
         "value": its,
@@ -239,18 +272,7 @@ def line_for(cid, args, with_cpu):
         "data": "synthetic (seeded mixture generator, flashgmm_amd/configs.py)",
         "config": {"workload": f"C{cid}: diag-cov GMM EM N={cfg.N} K={cfg.K} d={cfg.d} fp32",
                    "N": cfg.N, "K": cfg.K, "d": cfg.d, "kernel_variant": r["variant"]},
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "pass2 (gamma recompute + sufficient statistics)",
-            "achieved": achieved / 1e12,
-            "peak": FP32_PEAK / 1e12,
-            "unit": "TFLOP/s",
-            "frac": achieved / FP32_PEAK,
-            "traffic": measured_traffic(cid),
-            "traffic_unit": "bytes/launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE, profiles/)",
-            "peak_at_kernel_precision": pass2_peak() / 1e12,
-            "frac_at_kernel_precision": achieved / pass2_peak(),
-        },
+        "roofline": roof,
         "iteration_roofline_frac": roof_t / (sec / args.steps),
         "kernels_ms": {k: v["ms_avg"] for k, v in r["kernels"].items()},
         "ll_first": r["ll_first"],

@@ -38,11 +38,14 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // a 16x16 tile (K is padded to 32) and hold the 16-component coefficient
 // fragment in registers up to d = 128; below or above that the vector-ALU
 // kernels run.
-// From K >= 256 the x32 Pass 1 (fp32 candidates, exact log-normalizer) beats
-// the fp64 one by 20-27 % at d = 64 and 128 (measured; at K = 128 its
-// candidate work outweighs the saving), so auto pairs it with the fp64 Pass 2.
-static int resolve_variant(int K, int d, int variant) {
+// From K >= 128 the sparse variant (x32 Pass 1 listing each point's exact
+// pairs, statistics from those lists) beats the dense fp64 Pass 2 by
+// 1.1x (K = 128) to 2.5x (K = 512, N = 2^20) at d = 64 and 128 (measured);
+// it needs N * min(K, 32) < 2^31 and K <= 8192.
+static int resolve_variant(long N, int K, int d, int variant) {
   if (variant >= kValu && variant <= kSparse) return variant;
+  if (d <= 128 && K >= 128 && K <= 8192 && N * (long)(K < kSpCap ? K : kSpCap) < 2147483647L)
+    return kSparse;
   if (d <= 128 && K >= 256) return kMixed;
   if (d <= 128 && K >= 16) return kMfma;
   return kValu;
@@ -53,7 +56,7 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.N = N;
   g.K = K;
   g.d = d;
-  g.variant = resolve_variant(K, d, variant);
+  g.variant = resolve_variant(N, K, d, variant);
   if (g.variant == kMfma || g.variant == kX32 || both_sets(g.variant)) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
@@ -407,7 +410,7 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
 // Pass 2 from a caller's log-normalizer) run the fp64 matrix-core path.
 static int estep_variant(int K, int d, int variant) {
   if (variant < 0 || variant > kSparse) return variant;   // rejected by validate_shape
-  variant = resolve_variant(K, d, variant);
+  variant = resolve_variant(1, K, d, variant);   // N only decides sparse vs mixed
   return (variant == kX32 || both_sets(variant)) ? kMfma : variant;
 }
 
@@ -444,8 +447,9 @@ static size_t stream_acc_bytes(const Geom& g) {
 }
 static int stream_variant(int K, int d, int variant) {
   if (variant < 0 || variant > kSparse) return variant;   // rejected by validate_shape
-  variant = resolve_variant(K, d, variant);
-  return variant == kX32 ? kMfma : variant == kSparse ? kMixed : variant;
+  variant = resolve_variant(1, K, d, variant);
+  if (variant == kSparse) variant = K >= 256 ? kMixed : kMfma;
+  return variant == kX32 ? kMfma : variant;
 }
 
 }  // namespace fgmm
@@ -459,8 +463,7 @@ int fgmm_version(void) { return 100; }
 const char* fgmm_last_error(void) { return g_err; }
 
 int fgmm_resolve_variant(long N, int K, int d, int variant) {
-  (void)N;
-  return resolve_variant(K, d, variant);
+  return resolve_variant(N, K, d, variant);
 }
 
 size_t fgmm_workspace_bytes(long N, int K, int d, int variant) {

@@ -49,8 +49,11 @@ def test_version_and_variant_table(lib):
     assert lib.fgmm_version() >= 100
     # matrix cores from K >= 16 and d <= 128 (with the x32 log-normalizer
     # pass from K >= 256), vector ALU otherwise
-    assert lib.fgmm_resolve_variant(65536, 256, 128, 0) == 4
-    assert lib.fgmm_resolve_variant(262144, 128, 64, 0) == 2
+    assert lib.fgmm_resolve_variant(65536, 256, 128, 0) == 5
+    assert lib.fgmm_resolve_variant(262144, 128, 64, 0) == 5
+    assert lib.fgmm_resolve_variant(4096, 64, 32, 0) == 2
+    assert lib.fgmm_resolve_variant(65536, 9000, 64, 0) == 4        # K > 8192: mixed
+    assert lib.fgmm_resolve_variant(1 << 27, 256, 64, 0) == 4       # N * 32 >= 2^31
     assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 1
     assert lib.fgmm_resolve_variant(4096, 64, 200, 0) == 1
     assert lib.fgmm_resolve_variant(4096, 8, 32, 2) == 2
