@@ -126,7 +126,6 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   char* prow = take(sizeof(double) * npc * (size_t)g.stat_w);
   char* Xo = take(sizeof(float) * N * (size_t)g.d);
   char* ln2o = take(sizeof(double) * N);
-  char* part_sp = take(sizeof(double) * Kp * (size_t)g.stat_w);
   char* kmap = take(sizeof(int) * Kp);
   char* nflag = take(sizeof(int));
   char* Pf = take(sizeof(double) * 2 * Kp * (size_t)g.dp);
@@ -158,7 +157,6 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
     sp->prow = reinterpret_cast<double*>(prow);
     sp->Xo = reinterpret_cast<float*>(Xo);
     sp->ln2o = reinterpret_cast<double*>(ln2o);
-    sp->part_sp = reinterpret_cast<double*>(part_sp);
     sp->kmap = reinterpret_cast<int*>(kmap);
     sp->nflag = reinterpret_cast<int*>(nflag);
     sp->Pf = reinterpret_cast<double*>(Pf);
@@ -335,9 +333,10 @@ static int run_reduce(const Geom& g, const float* X, Ws& w, float* mu, float* va
   Timed t(3, s);
   if (g.variant == kSparse) {
     // stage 1 over the listed pairs' row and the overflow points' dense rows
-    int rc = check_hip(launch_reduce_sparse(g, w.sp.part_sp, 1, w.part, w.sp.nov, g.p2_chunk,
+    int rc = check_hip(launch_reduce_sparse(g, w.sp.prow, 1, w.part, w.sp.nov, g.p2_chunk,
                                             w.lnsum, mu, var, lp, params_next, bias_next,
-                                            ll_out, s, kReduceFlagging, w.x.flag),
+                                            ll_out, s, kReduceFlagging, w.x.flag, w.sp.pstart,
+                                            w.x.dmass, w.sp.glob),
                        "reduction / M-step");
     if (rc) return rc;
     // flagged components: all points, fp64 matrix cores, rows [s][k] of w.part

@@ -170,6 +170,7 @@ hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
 // and flags the component when any bound exceeds kX32Guard (a tenth of the
 // 1e-5 parity bar); its statistics are then recomputed exactly.
 constexpr double kX32Guard = 1e-6;
+constexpr int kReduceThreadsMax = 256;   // the sparse reductions run this many threads
 
 __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               int S, int stat_w, const double* __restrict__ part,
@@ -181,13 +182,16 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               double* __restrict__ P_next, double* __restrict__ bias_next,
                               double* __restrict__ ll_out, int standard, int stage,
                               int* __restrict__ flag, const double* __restrict__ part2,
-                              const int* __restrict__ ndyn, long chunk2) {
+                              const int* __restrict__ ndyn, long chunk2,
+                              const int* __restrict__ pstart, const float* __restrict__ dmass,
+                              int nblk, const double* __restrict__ glob) {
   __shared__ double red[16];
   __shared__ double nk_sh;
   __shared__ double errb_sh[3];
   __shared__ int bad_sh;
   __shared__ float mu_sh[kMaxD], var_sh[kMaxD];
   __shared__ double sa_sh[kMaxD], sb_sh[kMaxD];
+  __shared__ double hpa[kReduceThreadsMax], hpb[kReduceThreadsMax];
   const int k = blockIdx.x;
 
   if (stage == kReduceFlagged && (k >= K || flag[k] == 0)) return;
@@ -210,11 +214,24 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   // sparse variant: partial rows of the dense pass over the overflow points
   int S2 = 0;
   if (part2 != nullptr) S2 = (int)(((long)*ndyn + chunk2 - 1) / chunk2);
+  // rows of component k: part[s][k] for s < S, or (sparse, pstart) the
+  // contiguous piece rows pstart[k] .. pstart[k+1]
+  const double* pb = part + (size_t)k * row;
+  size_t kst = kstride;
+  int Sk = S;
+  if (pstart != nullptr) {   // a component with many pieces: every G-th row holds G rows' sums
+    const int r0 = pstart[k];
+    const int np = pstart[k + 1] - r0;
+    const int G = np > kSpFoldRows ? (np + kSpFoldRows - 1) / kSpFoldRows : 1;
+    Sk = (np + G - 1) / G;
+    pb = part + (size_t)r0 * row;
+    kst = row * G;
+  }
   {
     // n_k: chunk partials split across the block, merged in a fixed order
     double t = 0.0;
-    const double* p = part + (size_t)k * row + 2 * dp;
-    for (int s = threadIdx.x; s < S; s += blockDim.x) t += p[(size_t)s * kstride];
+    const double* p = pb + 2 * dp;
+    for (int s = threadIdx.x; s < Sk; s += blockDim.x) t += p[(size_t)s * kst];
     if (S2 > 0) {
       const double* p2 = part2 + (size_t)k * row + 2 * dp;
       for (int s = threadIdx.x; s < S2; s += blockDim.x) t += p2[(size_t)s * kstride];
@@ -223,9 +240,22 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     if (stage == kReduceFlagging) {
       for (int c = 1; c <= 3; c++) {
         double e = 0.0;
-        for (int s = threadIdx.x; s < S; s += blockDim.x) e += p[(size_t)s * kstride + c];
+        for (int s = threadIdx.x; s < Sk; s += blockDim.x) e += p[(size_t)s * kst + c];
         e = block_sum_f64(e, red);
         if (threadIdx.x == 0) errb_sh[c - 1] = e;
+      }
+      if (dmass != nullptr) {
+        // sparse: pairs that never became pending (Pass-1 workgroup bounds, in
+        // order), weighted by the global max |x| / x^2, plus the floor
+        double e = 0.0;
+        for (int b = threadIdx.x; b < nblk; b += blockDim.x) e += (double)dmass[(size_t)k * nblk + b];
+        e = block_sum_f64(e, red);
+        if (threadIdx.x == 0) {
+          const double dk = e * (1.0 + 0x1p-40) + glob[0];
+          errb_sh[0] += dk;
+          errb_sh[1] += dk * glob[1];
+          errb_sh[2] += dk * glob[2];
+        }
       }
     }
     if (threadIdx.x == 0) {
@@ -237,13 +267,53 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   const double nk = nk_sh;
   const double inv = standard ? 1.0 / nk : 1.0 / (nk > 1e-8 ? nk : 1e-8);
   const double ncl = nk > 1e-8 ? nk : 1e-8;
+  // column sums (sparse variant, blockDim >= 2d): the rows are split over H
+  // groups of d threads and the H partial sums combined in order
+  const int H = (variant == kSparse && (int)blockDim.x >= 2 * d) ? (int)blockDim.x / d : 1;
+  if (H > 1) {
+    const int jj = threadIdx.x % d, h = threadIdx.x / d;
+    double a = 0.0, b = 0.0;
+    if (h < H) {
+      int s = h;
+      for (; s + 7 * H < Sk; s += 8 * H) {   // eight rows in flight, summed in order
+        double va[8], vb[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          va[q] = pb[(size_t)(s + q * H) * kst + jj];
+          vb[q] = pb[(size_t)(s + q * H) * kst + dp + jj];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          a += va[q];
+          b += vb[q];
+        }
+      }
+      for (; s < Sk; s += H) {
+        a += pb[(size_t)s * kst + jj];
+        b += pb[(size_t)s * kst + dp + jj];
+      }
+      for (int s = h; s < S2; s += H) {
+        a += part2[(size_t)s * kstride + (size_t)k * row + jj];
+        b += part2[(size_t)s * kstride + (size_t)k * row + dp + jj];
+      }
+      hpa[h * d + jj] = a;
+      hpb[h * d + jj] = b;
+    }
+    __syncthreads();
+  }
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
     double a = 0.0, b = 0.0;
-    const double* p = part + (size_t)k * row;
+    const double* p = pb;
+    if (H > 1) {
+      for (int h = 0; h < H; h++) {
+        a += hpa[h * d + j];
+        b += hpb[h * d + j];
+      }
+    } else {
 #pragma unroll 8
-    for (int s = 0; s < S; s++) {
-      a += p[(size_t)s * kstride + j];
-      b += p[(size_t)s * kstride + dp + j];
+    for (int s = 0; s < Sk; s++) {
+      a += p[(size_t)s * kst + j];
+      b += p[(size_t)s * kst + dp + j];
     }
     if (S2 > 0) {
       const double* p2 = part2 + (size_t)k * row;
@@ -251,6 +321,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
         a += p2[(size_t)s * kstride + j];
         b += p2[(size_t)s * kstride + dp + j];
       }
+    }
     }
     sa_sh[j] = a;
     sb_sh[j] = b;
@@ -313,7 +384,8 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
-                     bias_next, ll_out, standard, stage, flag, nullptr, nullptr, 1L);
+                     bias_next, ll_out, standard, stage, flag, nullptr, nullptr, 1L, nullptr,
+                     nullptr, 0, nullptr);
   return hipGetLastError();
 }
 
@@ -321,15 +393,18 @@ hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const 
                                 const int* ndyn, long chunk2, const double* lnsum,
                                 float* new_mu, float* new_var, float* new_log_pi,
                                 double* params_next, double* bias_next, double* ll_out,
-                                hipStream_t s, int stage, int* flag) {
+                                hipStream_t s, int stage, int* flag, const int* pstart,
+                                const float* dmass, const double* glob) {
   if (g.variant != kSparse || stage == kReduceAll || flag == nullptr || S < 1 ||
-      g.stat_w < 2 * g.dp + 4 || (part2 != nullptr && (ndyn == nullptr || chunk2 < 1)))
+      g.stat_w < 2 * g.dp + 4 || (part2 != nullptr && (ndyn == nullptr || chunk2 < 1)) ||
+      (pstart != nullptr && (dmass == nullptr || glob == nullptr)))
     return hipErrorInvalidValue;
   const int blocks = (params_next != nullptr || stage == kReduceFlagging) ? g.Kp : g.K;
-  hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(128), 0, s, g.variant, g.N, g.K,
-                     g.Kp, g.d, g.dp, S, g.stat_w, part, lnsum, g.p1_blocks, nullptr,
+  hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(kReduceThreadsMax), 0, s, g.variant, g.N,
+                     g.K, g.Kp, g.d, g.dp, S, g.stat_w, part, lnsum, g.p1_blocks, nullptr,
                      nullptr, nullptr, new_mu, new_var, new_log_pi, params_next, bias_next,
-                     ll_out, 0, stage, flag, part2, ndyn, chunk2 < 1 ? 1L : chunk2);
+                     ll_out, 0, stage, flag, part2, ndyn, chunk2 < 1 ? 1L : chunk2, pstart,
+                     dmass, g.p1_blocks, glob);
   return hipGetLastError();
 }
 

@@ -113,6 +113,7 @@ constexpr int kSpCap = 32;            // list entries per point (at most K)
 constexpr int kSpPts = 256;           // points per sort chunk
 constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
 constexpr int kSpPiece = 64;          // entries per accumulation piece (at least)
+constexpr int kSpFoldRows = 64;       // a component's piece rows beyond this are summed in groups
 
 // Buffers of the sparse Pass 2 (see fgmm_sparse.hip).
 struct SpWs {
@@ -135,7 +136,6 @@ struct SpWs {
   double* prow;        // [npiece_cap][stat_w] piece sums
   float* Xo;           // [N][d] rows of the overflow points
   double* ln2o;        // [N] their log-normalizers
-  double* part_sp;     // [Kp][stat_w] statistics of the listed pairs
   int* kmap;           // [Kp] flagged components, compacted (-1 = padding)
   int* nflag;          // [1]
   double* Pf;          // fp64 fragment coefficients of the flagged components
@@ -221,16 +221,19 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                          float* new_var, float* new_log_pi, double* params_next,
                          double* bias_next, double* ll_out, hipStream_t s,
                          int standard = 0, int stage = kReduceAll, int* flag = nullptr);
-// Sparse variant: sums S rows of part, then the first ceil(*ndyn / chunk2)
-// rows of part2 (the dense pass over the overflow points; none if part2 is
-// null).  Error-bound columns come from part alone.
+// Sparse variant: sums S rows of part (or, with pstart, component k's piece
+// rows pstart[k] .. pstart[k+1] of part, plus the never-pending bounds dmass
+// and glob in the error columns), then the first ceil(*ndyn / chunk2) rows of
+// part2 (the dense pass over the overflow points; none if part2 is null).
+// Error-bound columns come from part alone.
 hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const double* part2,
                                 const int* ndyn, long chunk2, const double* lnsum,
                                 float* new_mu, float* new_var, float* new_log_pi,
                                 double* params_next, double* bias_next, double* ll_out,
-                                hipStream_t s, int stage, int* flag);
-// Sparse Pass 2: chunk sort, scan, placement (+ gather of the overflow
-// points), piece sums, fold into sp.part_sp.
+                                hipStream_t s, int stage, int* flag, const int* pstart = nullptr,
+                                const float* dmass = nullptr, const double* glob = nullptr);
+// Sparse Pass 2: chunk sort, scans, placement (+ gather of the overflow
+// points), piece sums (sp.prow, reduced per component by the reduction).
 hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, const SpWs& sp,
                                const double* ln2, hipStream_t s);
 // Flagged components (flag[k] != 0) compacted into sp.kmap / sp.nflag with

@@ -28,7 +28,8 @@
 //   sp_place_kernel   moves each chunk's sorted entries to their place;
 //                     copies the overflow points out
 //   sp_piece_kernel   fp64 sums over one piece per workgroup
-//   sp_fold_kernel    per component, the sum of its pieces in order
+//   sp_group_kernel   components with more than 64 pieces: groups of rows
+//                     summed in order; the reduction sums the rest in order
 //   sp_flag_kernel    flagged components -> compact list and coefficients
 //
 // Reference kernel this replaces (file:line in the reference repository):
@@ -48,6 +49,7 @@ constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
 constexpr int kAccUnroll = 4;      // entries per lane group in flight
+constexpr int kSpCountMax = 2048;  // up to this Kp the chunk sort is a counting sort
 constexpr int kPieceGrid = 2048;   // workgroups of the piece kernel (grid-stride)
 
 // exclusive scan over the workgroup (NT threads), one value per thread
@@ -137,6 +139,42 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
   const int cut = cut_sh;
   const int Ek = ek_sh;    // kept entries; after the sort they lead
   const int Ep = ep_sh;    // positions written
+  int2* out = blk + (size_t)ch * kSpChunkCap;
+  if (Kp <= kSpCountMax) {
+    // counting sort: run starts from the histogram; an entry's rank in its
+    // run = the number of the chunk's lower points listing the component
+    // (one bit per point and component)
+    unsigned long long* pm = reinterpret_cast<unsigned long long*>(hist + Kp);   // [Kp][4]
+    int* rs = reinterpret_cast<int*>(pm + 4 * (size_t)Kp);                      // [Kp]
+    for (int i = tid; i < 4 * Kp; i += kT) pm[i] = 0ull;
+    {
+      int carry = 0;   // exclusive scan of hist over k, kT at a time
+      for (int b = 0; b < Kp; b += kT) {
+        const int k = b + tid;
+        const int v = k < Kp ? hist[k] : 0;
+        int tot;
+        const int ex = block_excl_scan<kT>(v, sh, &tot);
+        if (k < Kp) rs[k] = carry + ex;
+        carry += tot;
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < Ep; i += kT) {
+      const int key = keys[i];
+      if (key != INT_MAX)
+        atomicOr(&pm[4 * (key >> kPointBits) + ((key & (kSpPts - 1)) >> 6)], 1ull << (key & 63));
+    }
+    __syncthreads();
+    for (int i = tid; i < Ep; i += kT) {
+      const int key = keys[i];
+      if (key == INT_MAX) continue;
+      const int k = key >> kPointBits, p = key & (kSpPts - 1), wi = p >> 6;
+      const unsigned long long* mk = pm + 4 * (size_t)k;
+      int rank = __popcll(mk[wi] & ((1ull << (p & 63)) - 1ull));
+      for (int q = 0; q < wi; q++) rank += __popcll(mk[q]);
+      out[rs[k] + rank] = make_int2(key, __float_as_int(vals[i]));
+    }
+  } else {
   int n2 = 2;
   while (n2 < Ep) n2 <<= 1;
   for (int i = Ep + tid; i < n2; i += kT) keys[i] = INT_MAX;
@@ -160,8 +198,8 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
       __syncthreads();
     }
   }
-  int2* out = blk + (size_t)ch * kSpChunkCap;
   for (int i = tid; i < Ek; i += kT) out[i] = make_int2(keys[i], __float_as_int(vals[i]));
+  }
   for (int k = tid; k < Kp; k += kT) cnt[(size_t)k * nchunk + ch] = hist[k];
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) s1 = fmax(s1, __shfl_xor(s1, off, 64));
@@ -430,52 +468,30 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
   }
 }
 
-// per component: its pieces summed in order, plus the bound columns
-__global__ __launch_bounds__(kT) void sp_fold_kernel(int d, int dp, int stat_w, int nblk,
-                                                     const int* __restrict__ pstart,
-                                                     const double* __restrict__ prow,
-                                                     const float* __restrict__ dmass,
-                                                     const double* __restrict__ glob,
-                                                     double* __restrict__ part_sp) {
-  __shared__ double red[kT / 64];
-  __shared__ double fsh[3];
-  const int k = blockIdx.x, tid = threadIdx.x;
-  {   // D_k: the Pass-1 workgroups' bounds ([component][workgroup]), fixed order
-    double t = 0.0;
-    const float* dk = dmass + (size_t)k * nblk;
-    for (int b = tid; b < nblk; b += kT) t += (double)dk[b];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = t;
-  }
-  const int r0 = pstart[k], r1 = pstart[k + 1];
-  double* out = part_sp + (size_t)k * stat_w;
-  // columns [0, d), [dp, dp + d), 2dp .. 2dp+3: one per thread, rows in order
-  for (int f = tid; f < 2 * dp + 4; f += kT) {
-    if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
-    double a = 0.0;
-    int r = r0;
-    for (; r + 8 <= r1; r += 8) {
-      double v[8];
-#pragma unroll
-      for (int q = 0; q < 8; q++) v[q] = prow[(size_t)(r + q) * stat_w + f];
-#pragma unroll
-      for (int q = 0; q < 8; q++) a += v[q];
+// A component with more than kSpFoldRows pieces: rows in groups of G =
+// ceil(pieces / kSpFoldRows), each group's sum (in order) written into its
+// first row, so the reduction reads at most kSpFoldRows rows per component.
+__global__ __launch_bounds__(kT) void sp_group_kernel(int d, int dp, int stat_w,
+                                                      const int* __restrict__ pstart,
+                                                      const int* __restrict__ pcomp,
+                                                      const int* __restrict__ nov,
+                                                      double* __restrict__ prow) {
+  const int npiece = nov[1];
+  for (int r = blockIdx.x; r < npiece; r += gridDim.x) {
+    const int k = pcomp[r];
+    const int r0 = pstart[k], np = pstart[k + 1] - r0;
+    if (np <= kSpFoldRows) continue;
+    const int G = (np + kSpFoldRows - 1) / kSpFoldRows;
+    const int i = r - r0;
+    if (i % G != 0) continue;
+    const int n = min(G, np - i);
+    double* out = prow + (size_t)r * stat_w;
+    for (int f = threadIdx.x; f < 2 * dp + 4; f += kT) {
+      if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
+      double a = out[f];
+      for (int q = 1; q < n; q++) a += out[(size_t)q * stat_w + f];
+      out[f] = a;
     }
-    for (; r < r1; r++) a += prow[(size_t)r * stat_w + f];
-    if (f <= 2 * dp) out[f] = a;
-    else fsh[f - 2 * dp - 1] = a;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    // bound entries (their own max|x|) + pairs that never became pending
-    // (the global max) + the floor
-    double t = 0.0;
-    for (int w = 0; w < kT / 64; w++) t += red[w];
-    const double dk = t * (1.0 + 0x1p-40) + glob[0];
-    out[2 * dp + 1] = fsh[0] + dk;
-    out[2 * dp + 2] = fsh[1] + dk * glob[1];
-    out[2 * dp + 3] = fsh[2] + dk * glob[2];
   }
 }
 
@@ -545,12 +561,15 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
       w.pv == nullptr || w.pcnt == nullptr || w.dmass == nullptr || w.pC != g.sp_C ||
       g.sp_C > kSpChunkCap)
     return hipErrorInvalidValue;
-  const size_t lds_sort = (2 * (size_t)kSpChunkCap + (size_t)g.Kp) * sizeof(int);
+  // keys, gamma, histogram; the counting sort adds a point bitmask (32 B) and
+  // a run start (4 B) per component
+  const size_t lds_sort = (2 * (size_t)kSpChunkCap + (size_t)g.Kp) * sizeof(int) +
+                          (g.Kp <= kSpCountMax ? 36 * (size_t)g.Kp : 0);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)sp_sort_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(2 * (size_t)kSpChunkCap + 8192) * (int)sizeof(int));
+    hipError_t e = hipFuncSetAttribute(
+        (const void*)sp_sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)((2 * (size_t)kSpChunkCap + 8192) * sizeof(int) + 36 * (size_t)kSpCountMax));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -575,8 +594,9 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   else if (g.dp <= 64) e = piece_launch<16>(g, X, sp, s);
   else e = piece_launch<32>(g, X, sp, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_fold_kernel, dim3(g.K), dim3(kT), 0, s, g.d, g.dp, g.stat_w,
-                     g.p1_blocks, sp.pstart, sp.prow, w.dmass, sp.glob, sp.part_sp);
+  const long cap = sp_npiece_cap(g);
+  hipLaunchKernelGGL(sp_group_kernel, dim3(cap < 2048 ? cap : 2048), dim3(kT), 0, s, g.d, g.dp,
+                     g.stat_w, sp.pstart, sp.pcomp, sp.nov, sp.prow);
   return hipGetLastError();
 }
 
