@@ -173,8 +173,12 @@ WsLayout make_layout(const Geom& g) {
   const bool xset = x32 || both;                       // holds the x32 coefficient set
   const size_t kd2 = 2 * (size_t)g.Kp * g.dp;
   L.params = off;
-  off = align256(off + sizeof(double) * kd2 * (both ? 2 : 1) +
-                 (xset ? sizeof(float) * kd2 : 0));
+  if (g.variant == kSparse)   // fp64 fragments, direct-form rows of dpb, bf16 splits
+    off = align256(off + sizeof(double) * kd2 + sizeof(double) * 2 * (size_t)g.Kp * sp_dpb(g.dp) +
+                   8 * (size_t)g.Kp * sp_dpb(g.dp));
+  else
+    off = align256(off + sizeof(double) * kd2 * (both ? 2 : 1) +
+                   (xset ? sizeof(float) * kd2 : 0));
   L.bias = off;
   off = align256(off + sizeof(double) * (size_t)g.Kp * (both ? 2 : 1) +
                  (xset ? 2 * sizeof(float) * (size_t)g.Kp : 0));
@@ -294,8 +298,9 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
        reinterpret_cast<double*>(b + L.part), X32Ws{}, SpWs{}, true};
   if (both_sets(g.variant)) {   // x32 set behind the fp64 one; no slots
     const size_t kd2 = 2 * (size_t)g.Kp * g.dp;
+    const size_t kv2 = 2 * (size_t)g.Kp * (g.variant == kSparse ? sp_dpb(g.dp) : g.dp);
     w.x.V = w.params + kd2;
-    w.x.P32 = reinterpret_cast<const float*>(w.params + 2 * kd2);
+    w.x.P32 = reinterpret_cast<const float*>(w.params + kd2 + kv2);
     w.x.b64 = w.bias + g.Kp;
     w.x.bias32 = reinterpret_cast<const float*>(w.bias + 2 * g.Kp);
     w.x.Z32 = w.x.bias32 + g.Kp;

@@ -7,6 +7,8 @@
 #include <float.h>
 #include <math.h>
 
+#include <hip/hip_bf16.h>
+
 #include "fgmm_internal.h"
 
 namespace fgmm {
@@ -65,12 +67,16 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
   const int Q = dp / 4, S1 = dp / 2;
   const bool mf = variant == kMfma || both_sets(variant);   // fp64 fragment set
   const bool xf = variant == kX32 || both_sets(variant);    // x32 set
+  // kSparse: direct-form rows of dpb features in octet order and bf16 split
+  // fragments instead of the fp32 ones (its Pass 1 runs on bf16 matrix cores)
+  const bool sp = variant == kSparse;
+  const int dpb = sp ? sp_dpb(dp) : dp;
   // kMixed and kSparse keep the x32 set behind the fp64 fragment set (and its
   // direct bias behind the expanded one)
   double* Vx = both_sets(variant) ? P + 2 * (size_t)Kp * dp : P;
-  float* P32 = reinterpret_cast<float*>(Vx + 2 * (size_t)Kp * dp);
+  float* P32 = reinterpret_cast<float*>(Vx + 2 * (size_t)Kp * dpb);
   double* bx = both_sets(variant) ? bias + Kp : bias;
-  for (int j = threadIdx.x; j < dp; j += blockDim.x) {
+  for (int j = threadIdx.x; j < dpb; j += blockDim.x) {
     double iv = 0.0, mu = 0.0;
     if (real && j < d) {
       double vv = (double)v[j];
@@ -81,11 +87,34 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
     }
     const int ks = k >> 4, c = k & 15, g = j / Q, t = j - g * Q;
     const int lane = 16 * g + c;
-    if (mf) {
+    if (mf && j < dp) {
       P[((size_t)ks * S1 + t) * 64 + lane] = -0.5 * kLog2e * iv;
       P[((size_t)ks * S1 + Q + t) * 64 + lane] = kLog2e * mu * iv;
     }
-    if (xf) {
+    if (sp) {
+      // octet order: lane group g holds features 32u + 8g + v (v < 8) as its
+      // t-th feature, t = 8u + v, at position 4t + g
+      const int gg = (j & 31) >> 3, tt = 8 * (j >> 5) + (j & 7);
+      const double sc = sqrt(0.5 * kLog2e * iv);
+      const size_t pos = (size_t)k * dpb + 4 * tt + gg;
+      Vx[2 * pos] = sc;
+      Vx[2 * pos + 1] = mu * sc;
+      // bf16 fragments [ks][step][hi, lo][lane][8]: step s < dpb/32 holds the
+      // x^2 coefficients of features 32s .. 32s+31, step dpb/32 + s the x ones;
+      // lane 16 g' + c holds features 32s + 8g' .. +7 of component 16 ks + c
+      __bf16* B16 = reinterpret_cast<__bf16*>(P32);
+      const int SX = dpb / 32, SS = 2 * SX;
+      const int ln = 16 * gg + c, v = j & 7;
+      const float fa = (float)(-0.5 * kLog2e * iv), fb = (float)(kLog2e * mu * iv);
+      const __bf16 ah = (__bf16)fa, al = (__bf16)(fa - (float)ah);
+      const __bf16 bh = (__bf16)fb, bl = (__bf16)(fb - (float)bh);
+      auto at = [&](int st, int h) { return ((((size_t)ks * SS + st) * 2 + h) * 64 + ln) * 8 + v; };
+      B16[at(j >> 5, 0)] = ah;
+      B16[at(j >> 5, 1)] = al;
+      B16[at(SX + (j >> 5), 0)] = bh;
+      B16[at(SX + (j >> 5), 1)] = bl;
+    }
+    if (xf && !sp && j < dp) {
       // quarter-interleaved: feature j = g*Q + t at position 4t + g
       double sc = sqrt(0.5 * kLog2e * iv);
       const size_t pos = (size_t)k * dp + 4 * t + g;
@@ -97,7 +126,7 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
       P[(size_t)k * dp + j] = sc;
       P[(size_t)Kp * dp + (size_t)k * dp + j] = mu * sc;
     }
-    if (xf) {
+    if (xf && !sp) {
       P32[((size_t)ks * S1 + t) * 64 + lane] = (float)(-0.5 * kLog2e * iv);
       P32[((size_t)ks * S1 + Q + t) * 64 + lane] = (float)(kLog2e * mu * iv);
     }
@@ -122,7 +151,7 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
         const double be = kLog2e * (lc - 0.5 * q);
         bias32[k] = (float)be;
         // |bias| + D_k, D_k = 0.5 log2(e) sum mu^2/var; rounded up to fp32
-        const double z = x32_err_c(dp) * (fabs(be) + 0.5 * kLog2e * q);
+        const double z = (sp ? x32_err_c_bf(dpb) : x32_err_c(dp)) * (fabs(be) + 0.5 * kLog2e * q);
         Z32[k] = (float)(z * (1.0 + 1e-6));
       }
     }

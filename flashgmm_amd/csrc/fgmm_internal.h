@@ -158,6 +158,23 @@ inline long sp_npiece_cap(const Geom& g) { return sp_piece_budget(g) + g.Kp + 1;
 // D_k) is precomputed per component; the slope on |a0| is 2c.
 constexpr double kU32 = 5.9604644775390625e-8;  // 2^-24
 __host__ __device__ constexpr double x32_err_c(int dp) { return (2.0 * dp + 8.0) * kU32; }
+// The sparse variant's Pass 1 runs the same contraction on bf16 matrix cores
+// with each operand split into two bf16 parts, a = a1 + a2 (|a - a1 - a2| <=
+// 2^-16 |a|), and three products a1 b1 + a1 b2 + a2 b1 per term (the dropped
+// a2 b2 <= 2^-16 |ab|); each product of bf16 parts is exact in fp32 and the
+// accumulation (3 dpb products per accumulator, dpb = d padded to 32) rounds
+// like the fp32 one.  So every term carries <= 3 2^-16 + 2 2^-24 relative
+// error and the chained additions (3 dpb + 8) 2^-24 of the sum of |terms|:
+//     |ll_bf - ll2| <= c_bf (|bias_k| + D_k + 2 |a0|),
+//     c_bf = 2 (3 2^-16 + (3 dpb + 8) 2^-24)          (doubled for margin).
+// (Measured on gfx950: max error 3.5e-6 of sum |terms| at 256 features,
+// against 6.9e-5 before doubling.)
+__host__ __device__ constexpr double x32_err_c_bf(int dpb) {
+  return 2.0 * (3.0 * 0x1p-16 + (3.0 * dpb + 8.0) * kU32);
+}
+// Feature padding of the bf16 layout: the x^2 and x halves each fill whole
+// 32-feature steps of the 16x16x32 instruction.
+__host__ __device__ constexpr int sp_dpb(int dp) { return (dp + 31) / 32 * 32; }
 
 // sum_j (x_j s_kj - mu_kj s_kj)^2 over j < d in fp64 from the direct-form
 // coefficients of the x32 variant: V2 holds (s, mu s) pairs, feature

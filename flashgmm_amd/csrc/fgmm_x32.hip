@@ -46,6 +46,7 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kW1 = 8;                  // Pass 1 wavefronts per workgroup
 constexpr int kPts1 = 16 * kW1;         // Pass 1 points per workgroup
@@ -60,6 +61,11 @@ constexpr int kSlots = kX32Slots;       // slots per point (4 per lane group)
 static_assert(kSlots == 16, "Pass 1 writes 4 slots per lane group, Pass 2 reads 2 x uint4");
 constexpr unsigned short kNoSlot = 0xFFFF;
 constexpr int kX1Slots = 0, kX1Plain = 1, kX1Emit = 2;   // Pass-1 output modes
+// floats per 32-component coefficient tile: fp32 fragments, or (EMIT) bf16
+// hi/lo fragments over dpb features
+constexpr int x1_tile_floats(int dp, int mode) {
+  return mode == kX1Emit ? sp_dpb(dp) * 64 : kSub1 * (dp / 2) * 64;
+}
 // EMIT: pending pairs that end up less than this far below the window are
 // listed as bound entries (those further down have gamma < 2^-(kWin +
 // kSpKeep) = 2^-126)
@@ -80,6 +86,38 @@ __device__ inline f32x4 mfma32(float a, float b, f32x4 c) {
 }
 __device__ inline f64x4 mfma64(double a, double b, f64x4 c) {
   return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// x[n][32u + 8g .. 32u + 8g + 7] for u < QX/8 as xq[8u .. 8u+7] (octet order
+// of the bf16 sweep), zero beyond d or N.
+template <int QX, bool VEC>
+__device__ inline void load_octets32(const float* __restrict__ X, long n, long N, int d, int g,
+                                     float (&xq)[QX]) {
+#pragma unroll
+  for (int u = 0; u < QX / 8; u++) {
+    const int j0 = 32 * u + 8 * g;
+    if (VEC && n < N && j0 + 8 <= d) {
+      const float4* p = reinterpret_cast<const float4*>(X + (size_t)n * d + j0);
+      const float4 a = p[0], b = p[1];
+      xq[8 * u] = a.x; xq[8 * u + 1] = a.y; xq[8 * u + 2] = a.z; xq[8 * u + 3] = a.w;
+      xq[8 * u + 4] = b.x; xq[8 * u + 5] = b.y; xq[8 * u + 6] = b.z; xq[8 * u + 7] = b.w;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int j = j0 + t;
+        xq[8 * u + t] = (n < N && j < d) ? X[(size_t)n * d + j] : 0.f;
+      }
+    }
+  }
+}
+
+__device__ inline void split_bf16(float v, __bf16& h, __bf16& l) {
+  h = (__bf16)v;
+  l = (__bf16)(v - (float)h);
+}
+
+__device__ inline f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 template <int Q, bool VEC>
@@ -120,11 +158,17 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
     int* __restrict__ pcnt, int pC, float* __restrict__ dmass) {
   constexpr bool SLOTS = MODE == kX1Slots, EMIT = MODE == kX1Emit;
   constexpr float kWinP1 = kWin;
+  // EMIT (sparse variant): the sweep runs on bf16 matrix cores with split
+  // operands (x32_err_c_bf); features in octet order, padded to DPB
+  constexpr bool BF = EMIT;
+  constexpr int DPB = sp_dpb(DP), SX = DPB / 32, SS = 2 * SX;
   constexpr int Q = DP / 4, S1 = DP / 2;
-  constexpr int TILE = kSub1 * S1 * 64;                 // floats per K tile
+  constexpr int QX = BF ? DPB / 4 : Q;                  // features per lane
+  constexpr int VROW = BF ? DPB : DP;                   // direct-form row length
+  constexpr int TILE = x1_tile_floats(DP, MODE);        // floats per K tile
   constexpr int TV4 = TILE / 4;                         // float4 per tile
   constexpr int PER = (TV4 + kThr1 - 1) / kThr1;
-  constexpr float Wslope = (float)(2.0 * x32_err_c(DP));
+  constexpr float Wslope = (float)(2.0 * (BF ? x32_err_c_bf(DPB) : x32_err_c(DP)));
   extern __shared__ float smemf[];                      // [2][TILE], int2 [kPendL][512]
   __shared__ float sB[2][16 * kSub1], sZ[2][16 * kSub1];
   __shared__ double red[kW1];
@@ -136,11 +180,31 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   const long n = (long)blockIdx.x * kPts1 + wave * 16 + c;
   const bool valid = n < N;
 
-  float xq[Q];
-  load_quarter32<Q, VEC>(X, n, N, d, g * Q, xq);
+  float xq[QX];
+  if (BF) load_octets32<QX, VEC>(X, n, N, d, g, xq);
+  else load_quarter32<QX, VEC>(X, n, N, d, g * Q, xq);
   float xmax2 = 0.f;   // max_j x_j^2 of the point
 #pragma unroll
-  for (int j = 0; j < Q; j++) xmax2 = fmaxf(xmax2, xq[j] * xq[j]);
+  for (int j = 0; j < QX; j++) xmax2 = fmaxf(xmax2, xq[j] * xq[j]);
+  // BF: the B operands, x^2 (fp32-rounded) and x split into bf16 hi + lo;
+  // step s of lane group g holds features 32s + 8g .. +7
+  bf16x8 x2h[BF ? SX : 1], x2l[BF ? SX : 1], x1h[BF ? SX : 1], x1l[BF ? SX : 1];
+  if (BF) {
+#pragma unroll
+    for (int u = 0; u < SX; u++) {
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const float x = xq[8 * u + t];
+        __bf16 h, l;
+        split_bf16(x * x, h, l);
+        x2h[u][t] = h;
+        x2l[u][t] = l;
+        split_bf16(x, h, l);
+        x1h[u][t] = h;
+        x1l[u][t] = l;
+      }
+    }
+  }
   xmax2 = fmaxf(xmax2, __shfl_xor(xmax2, 16, 64));
   xmax2 = fmaxf(xmax2, __shfl_xor(xmax2, 32, 64));
 
@@ -243,8 +307,8 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
       if (go_) {                                                                      \
         k_ = plist[i_ * kThr1 + wave * 64 + gs_ * 16 + c].x;                          \
         const double2* cf_ =                                                          \
-            reinterpret_cast<const double2*>(V2) + (size_t)k_ * DP + g;               \
-        _Pragma("unroll") for (int j_ = 0; j_ < Q; j_++) {                            \
+            reinterpret_cast<const double2*>(V2) + (size_t)k_ * VROW + g;             \
+        _Pragma("unroll") for (int j_ = 0; j_ < QX; j_++) {                           \
           const double2 sm_ = cf_[4 * j_];                                            \
           const double t_ = fma((double)xq[j_], sm_.x, -sm_.y);                       \
           q_ = fma(t_, t_, q_);                                                       \
@@ -289,17 +353,48 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
       l0[r] = sB[buf][4 * g + r];
       l1[r] = sB[buf][16 + 4 * g + r];
     }
+    if (BF) {
+      // per step: lo*hi + hi*lo + hi*hi of the split operands
+      const bf16x8* sPb = reinterpret_cast<const bf16x8*>(sP);
 #pragma unroll
-    for (int s = 0; s < Q; s++) {
-      const float b = xq[s] * xq[s];
-      q0 = mfma32(sP[(0 * S1 + s) * 64 + lane], b, q0);
-      q1 = mfma32(sP[(1 * S1 + s) * 64 + lane], b, q1);
-    }
+      for (int u = 0; u < SX; u++) {
+        const bf16x8 a0h = sPb[((0 * SS + u) * 2 + 0) * 64 + lane];
+        const bf16x8 a0l = sPb[((0 * SS + u) * 2 + 1) * 64 + lane];
+        const bf16x8 a1h = sPb[((1 * SS + u) * 2 + 0) * 64 + lane];
+        const bf16x8 a1l = sPb[((1 * SS + u) * 2 + 1) * 64 + lane];
+        q0 = mfma_bf16(a0l, x2h[u], q0);
+        q1 = mfma_bf16(a1l, x2h[u], q1);
+        q0 = mfma_bf16(a0h, x2l[u], q0);
+        q1 = mfma_bf16(a1h, x2l[u], q1);
+        q0 = mfma_bf16(a0h, x2h[u], q0);
+        q1 = mfma_bf16(a1h, x2h[u], q1);
+      }
 #pragma unroll
-    for (int s = Q; s < S1; s++) {
-      const float b = xq[s - Q];
-      l0 = mfma32(sP[(0 * S1 + s) * 64 + lane], b, l0);
-      l1 = mfma32(sP[(1 * S1 + s) * 64 + lane], b, l1);
+      for (int u = 0; u < SX; u++) {
+        const bf16x8 a0h = sPb[((0 * SS + SX + u) * 2 + 0) * 64 + lane];
+        const bf16x8 a0l = sPb[((0 * SS + SX + u) * 2 + 1) * 64 + lane];
+        const bf16x8 a1h = sPb[((1 * SS + SX + u) * 2 + 0) * 64 + lane];
+        const bf16x8 a1l = sPb[((1 * SS + SX + u) * 2 + 1) * 64 + lane];
+        l0 = mfma_bf16(a0l, x1h[u], l0);
+        l1 = mfma_bf16(a1l, x1h[u], l1);
+        l0 = mfma_bf16(a0h, x1l[u], l0);
+        l1 = mfma_bf16(a1h, x1l[u], l1);
+        l0 = mfma_bf16(a0h, x1h[u], l0);
+        l1 = mfma_bf16(a1h, x1h[u], l1);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < Q; s++) {
+        const float b = xq[s] * xq[s];
+        q0 = mfma32(sP[(0 * S1 + s) * 64 + lane], b, q0);
+        q1 = mfma32(sP[(1 * S1 + s) * 64 + lane], b, q1);
+      }
+#pragma unroll
+      for (int s = Q; s < S1; s++) {
+        const float b = xq[s - Q];
+        l0 = mfma32(sP[(0 * S1 + s) * 64 + lane], b, l0);
+        l1 = mfma32(sP[(1 * S1 + s) * 64 + lane], b, l1);
+      }
     }
     float hi[8];
     float lmax = -FLT_MAX;
@@ -783,7 +878,7 @@ __global__ __launch_bounds__(256) void x32_fix_kernel(
 template <int DP, bool VEC, int MODE>
 hipError_t x1_launch_mode(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                           float* ln_out, double* lnsum, hipStream_t s) {
-  constexpr size_t lds = 2 * (size_t)kSub1 * (DP / 2) * 64 * sizeof(float) +
+  constexpr size_t lds = 2 * (size_t)x1_tile_floats(DP, MODE) * sizeof(float) +
                          (size_t)kPendL * kThr1 * sizeof(int2);
   static bool attr_set = false;
   if (!attr_set) {
