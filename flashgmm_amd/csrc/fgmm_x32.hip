@@ -246,8 +246,77 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   int sk4[4] = {-1, -1, -1, -1};
   int pc = 0;                             // EMIT: entries of this point's list so far
   const size_t pbase = (size_t)(valid ? n : 0) * pC;
+  // Exact evaluation of the live entries without slots: the entries of the
+  // wavefront's 16 points form one queue (point-major, then lane group, then
+  // list order) that the 16 lane columns share, so a round evaluates 16
+  // entries whichever points they belong to.  Column s takes item 16r + s
+  // (the last item again once the queue is spent, its result unused), finds
+  // the owning point p by binary search over the inclusive prefix counts,
+  // reads the component from p's list and p's features from lane (g, p) of
+  // its own row; two shuffles complete the distance.  The value goes back
+  // into the list slot it came from, and every lane then folds its own
+  // entries in list order into its sums.
+#define FGMM_X1_EVAL_QUEUE                                                            \
+  {                                                                                   \
+    int incl_ = tot_;                                                                 \
+    _Pragma("unroll") for (int o_ = 1; o_ < 16; o_ <<= 1) {                           \
+      const int u_ = __shfl_up(incl_, o_, 16);                                        \
+      if (c >= o_) incl_ += u_;                                                       \
+    }                                                                                 \
+    const int T_ = __shfl(incl_, 15, 16);                                             \
+    const int pack_ = c0_ | (c1_ << 8) | (c2_ << 16);                                 \
+    const int rounds_ = (T_ + 15) >> 4;                                               \
+    for (int r_ = 0; r_ < rounds_; r_++) {                                            \
+      const int it_ = min(16 * r_ + c, T_ - 1);                                       \
+      int p_ = 0, b_ = 0;                                                             \
+      _Pragma("unroll") for (int s_ = 8; s_ >= 1; s_ >>= 1) {                         \
+        const int w_ = __shfl(incl_, p_ + s_ - 1, 16);                                \
+        if (w_ <= it_) {                                                              \
+          p_ += s_;                                                                   \
+          b_ = w_;                                                                    \
+        }                                                                             \
+      }                                                                               \
+      const int pq_ = __shfl(pack_, p_, 16);                                          \
+      const int pcp_ = __shfl(pc, p_, 16);                                            \
+      const int e_ = it_ - b_;                                                        \
+      const int q0_ = pq_ & 255, q1_ = (pq_ >> 8) & 255, q2_ = (pq_ >> 16) & 255;      \
+      const int gs_ = e_ < q0_ ? 0 : (e_ < q0_ + q1_ ? 1 : (e_ < q0_ + q1_ + q2_ ? 2 : 3)); \
+      const int ix_ = e_ - (gs_ > 0 ? q0_ : 0) - (gs_ > 1 ? q1_ : 0) - (gs_ > 2 ? q2_ : 0); \
+      const int a_ = ix_ * kThr1 + wave * 64 + gs_ * 16 + p_;                         \
+      const int k_ = plist[a_].x;                                                     \
+      const double2* cf_ = reinterpret_cast<const double2*>(V2) + (size_t)k_ * VROW + g; \
+      double q_ = 0.0;                                                                \
+      _Pragma("unroll") for (int j_ = 0; j_ < QX; j_++) {                             \
+        const float xv_ = __shfl(xq[j_], p_, 16);                                     \
+        const double2 sm_ = cf_[4 * j_];                                              \
+        const double t_ = fma((double)xv_, sm_.x, -sm_.y);                            \
+        q_ = fma(t_, t_, q_);                                                         \
+      }                                                                               \
+      q_ += __shfl_xor(q_, 16, 64);                                                   \
+      q_ += __shfl_xor(q_, 32, 64);                                                   \
+      const double v_ = b64[k_] - q_;                                                 \
+      if (g == 0 && 16 * r_ + c < T_) {                                               \
+        reinterpret_cast<double*>(plist)[a_] = v_;                                    \
+        if (EMIT && pcp_ + e_ < pC) {                                                 \
+          const size_t pb_ = (size_t)((long)blockIdx.x * kPts1 + wave * 16 + p_) * pC; \
+          pk[pb_ + pcp_ + e_] = k_;                                                   \
+          pv[pb_ + pcp_ + e_] = v_;                                                   \
+        }                                                                             \
+      }                                                                               \
+    }                                                                                 \
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");                            \
+    __builtin_amdgcn_wave_barrier();                                                  \
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");                            \
+    for (int i_ = 0; i_ < live_; i_++) {                                              \
+      const double v_ = reinterpret_cast<const double*>(plist)[i_ * kThr1 + tid];     \
+      const double mn_ = fmax(eM, v_);                                                \
+      eS = eS * (double)exp2f((float)(eM - mn_)) + (double)exp2f((float)(v_ - mn_));  \
+      eM = mn_;                                                                       \
+    }                                                                                 \
+  }
   // Evaluates the pending pairs still inside the window and empties the
-  // lists.  Wavefront-uniform.  The live entries of a point's four lanes
+  // lists.  Wavefront-uniform.  Without slots the live entries run through
+  // FGMM_X1_EVAL_QUEUE.  With slots the live entries of a point's four lanes
   // form one queue; round r evaluates every point's r-th entry: its four
   // lanes each compute their quarter of the fp64 distance, two shuffles
   // complete it, and the lane whose list held the entry folds the exact value
@@ -295,6 +364,9 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
     const int c0_ = __shfl(live_, c, 64), c1_ = __shfl(live_, 16 + c, 64);            \
     const int c2_ = __shfl(live_, 32 + c, 64), c3_ = __shfl(live_, 48 + c, 64);       \
     const int tot_ = c0_ + c1_ + c2_ + c3_;                                           \
+    if (!SLOTS) {                                                                     \
+      FGMM_X1_EVAL_QUEUE                                                              \
+    } else {                                                                          \
     int rounds_ = tot_;                                                               \
     _Pragma("unroll") for (int o_ = 32; o_ >= 1; o_ >>= 1)                            \
         rounds_ = max(rounds_, __shfl_xor(rounds_, o_, 64));                          \
@@ -332,11 +404,8 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
             }                                                                         \
           }                                                                           \
         }                                                                             \
-        if (EMIT && pc + r_ < pC) {                                                   \
-          pk[pbase + pc + r_] = k_;                                                   \
-          pv[pbase + pc + r_] = v_;                                                   \
-        }                                                                             \
       }                                                                               \
+    }                                                                                 \
     }                                                                                 \
     pc += tot_;                                                                       \
     npend = 0;                                                                        \
@@ -465,6 +534,7 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
   }
   FGMM_X1_FLUSH(Mrun - kWinP1)
 #undef FGMM_X1_FLUSH
+#undef FGMM_X1_EVAL_QUEUE
 
   // merge the exact sums of the four lane groups of each point
 #pragma unroll
