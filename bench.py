@@ -38,6 +38,7 @@ from flashgmm_amd.configs import CONFIGS, make_problem  # noqa: E402
 HBM_PEAK = 8.0e12        # B/s, MI355X
 FP32_PEAK = 157.3e12     # FLOP/s, MI355X dense fp32 (vector = matrix)
 FP64_PEAK = 78.6e12      # FLOP/s, MI355X dense fp64 (vector = matrix)
+BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 matrix cores
 
 
 def parse():
@@ -79,27 +80,41 @@ def pass2_peak() -> float:
     return 8.0 / (6.0 / FP64_PEAK + 2.0 / FP32_PEAK)
 
 
-FP32_SWEEP = ("x32", "mixed", "sparse")   # Pass 1 on fp32 matrix cores
+FP32_SWEEP = ("x32", "mixed")   # Pass 1 on fp32 matrix cores
+BF16_SWEEP = ("sparse",)        # Pass 1 on bf16 matrix cores, operands split hi + lo
 
 
 def dominant_roofline(cfg, variant, kernels):
     """Roofline of the kernel that takes the most time per iteration.
 
     Pass 1 is a dense sweep over all (n, k): 4 flops per (n, k, j) (the
-    x^2 and x contractions), on fp32 matrix cores for the x32-based variants
-    and on fp64 matrix cores (fp64 VALU for valu) otherwise.  The dense Pass 2
-    recomputes the distance and accumulates gamma^T [X, X^2]: 8 flops per
-    (n, k, j) at its fp64/fp32 instruction mix.  The sparse variant's Pass 2
-    touches only the listed pairs and is not dominant."""
+    x^2 and x contractions), on fp32 matrix cores for x32 and mixed, on fp64
+    matrix cores (fp64 VALU for valu) for mfma/valu, and for sparse on bf16
+    matrix cores with each operand split into bf16 hi + lo, three products
+    (lo*hi, hi*lo, hi*hi) per algorithmic product.  The metric prices the
+    algorithmic 4NKd against the fp32 matrix-core peak; for the bf16 sweep
+    the issued matrix-core work (3 x 4NKd) against the bf16 peak is reported
+    beside it.  The dense Pass 2 recomputes the distance and accumulates
+    gamma^T [X, X^2]: 8 flops per (n, k, j) at its fp64/fp32 instruction mix.
+    The sparse variant's Pass 2 touches only the listed pairs and is not
+    dominant."""
     nkd = float(cfg.N) * cfg.K * cfg.d
     t1 = kernels["pass1"]["ms_avg"] / 1e3
     t2 = kernels["pass2"]["ms_avg"] / 1e3
     if variant == "sparse" or t1 >= t2:
-        peak = FP32_PEAK if variant in FP32_SWEEP else FP64_PEAK
+        if variant in BF16_SWEEP:
+            peak, unit = FP32_PEAK, "bf16 matrix cores, split operands"
+        elif variant in FP32_SWEEP:
+            peak, unit = FP32_PEAK, "fp32 matrix cores"
+        else:
+            peak, unit = FP64_PEAK, "fp64"
         flops, t = 4.0 * nkd, t1
-        out = {"kernel": "pass1 (log-normalizer sweep, "
-                         + ("fp32 matrix cores" if variant in FP32_SWEEP else "fp64") + ")",
-               "peak": peak / 1e12}
+        out = {"kernel": f"pass1 (log-normalizer sweep, {unit})", "peak": peak / 1e12}
+        if variant in BF16_SWEEP and t > 0:
+            issued = 3.0 * flops
+            out["issued_bf16_mfma"] = {"flops_per_launch": issued,
+                                       "achieved": issued / t / 1e12, "peak": BF16_PEAK / 1e12,
+                                       "unit": "TFLOP/s", "frac": issued / t / BF16_PEAK}
     else:
         flops, t = 8.0 * nkd, t2
         peak = FP32_PEAK

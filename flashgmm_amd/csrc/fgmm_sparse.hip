@@ -19,8 +19,9 @@
 //
 // Kernels of one Pass 2 (all orders fixed, so results are reproducible):
 //   sp_sort_kernel    chunk of 256 points: its entries (gamma formed here)
-//                     bitonic-sorted in LDS by (component, point); counts per
-//                     component
+//                     sorted in LDS by (component, point) -- counting sort
+//                     over per-component point bitmasks for Kp <= 2048,
+//                     bitonic beyond; counts per component
 //   sp_rowscan_kernel per component, exclusive scan of its chunk counts
 //   sp_top_kernel     runs (each component's entries become one contiguous
 //                     run ordered by point), accumulation pieces of >= 64
