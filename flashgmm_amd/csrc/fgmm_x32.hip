@@ -284,13 +284,30 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
       const int ix_ = e_ - (gs_ > 0 ? q0_ : 0) - (gs_ > 1 ? q1_ : 0) - (gs_ > 2 ? q2_ : 0); \
       const int a_ = ix_ * kThr1 + wave * 64 + gs_ * 16 + p_;                         \
       const int k_ = plist[a_].x;                                                     \
-      const double2* cf_ = reinterpret_cast<const double2*>(V2) + (size_t)k_ * VROW + g; \
       double q_ = 0.0;                                                                \
-      _Pragma("unroll") for (int j_ = 0; j_ < QX; j_++) {                             \
-        const float xv_ = __shfl(xq[j_], p_, 16);                                     \
-        const double2 sm_ = cf_[4 * j_];                                              \
-        const double t_ = fma((double)xv_, sm_.x, -sm_.y);                            \
-        q_ = fma(t_, t_, q_);                                                         \
+      if (BF) {   /* (s fp64, mu fp32) rows: t = (x - mu) s, x - mu exact */            \
+        const double2* cs_ = reinterpret_cast<const double2*>(V2) + (size_t)k_ * (DPB / 2) + g; \
+        const float4* cm_ =                                                           \
+            reinterpret_cast<const float4*>(V2 + (size_t)Kp * DPB) + (size_t)k_ * (DPB / 4) + g; \
+        _Pragma("unroll") for (int w_ = 0; w_ < QX / 4; w_++) {                       \
+          const float4 m_ = cm_[4 * w_];                                              \
+          const double2 sa_ = cs_[8 * w_], sb_ = cs_[8 * w_ + 4];                     \
+          const float mv_[4] = {m_.x, m_.y, m_.z, m_.w};                              \
+          const double sv_[4] = {sa_.x, sa_.y, sb_.x, sb_.y};                         \
+          _Pragma("unroll") for (int i4_ = 0; i4_ < 4; i4_++) {                       \
+            const float xv_ = __shfl(xq[4 * w_ + i4_], p_, 16);                       \
+            const double t_ = ((double)xv_ - (double)mv_[i4_]) * sv_[i4_];            \
+            q_ = fma(t_, t_, q_);                                                     \
+          }                                                                           \
+        }                                                                             \
+      } else {                                                                        \
+        const double2* cf_ = reinterpret_cast<const double2*>(V2) + (size_t)k_ * VROW + g; \
+        _Pragma("unroll") for (int j_ = 0; j_ < QX; j_++) {                           \
+          const float xv_ = __shfl(xq[j_], p_, 16);                                   \
+          const double2 sm_ = cf_[4 * j_];                                            \
+          const double t_ = fma((double)xv_, sm_.x, -sm_.y);                          \
+          q_ = fma(t_, t_, q_);                                                       \
+        }                                                                             \
       }                                                                               \
       q_ += __shfl_xor(q_, 16, 64);                                                   \
       q_ += __shfl_xor(q_, 32, 64);                                                   \
@@ -498,7 +515,9 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
       bool any = false;
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        dv[u] = (valid && !(cm & (1u << u))) ? exp2f(hi[u] - Mrun) : 0.f;
+        // v_exp_f32 without range scaling: a result below 2^-126 may flush
+        // to zero, which the per-component floor N 2^-126 covers
+        dv[u] = (valid && !(cm & (1u << u))) ? __builtin_amdgcn_exp2f(hi[u] - Mrun) : 0.f;
         any = any || dv[u] > 0.f;
       }
       if (__ballot(any) != 0ull) {
