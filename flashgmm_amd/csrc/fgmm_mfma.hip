@@ -520,7 +520,9 @@ static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
                             const int* kmap = nullptr, const int* kdyn = nullptr) {
   const int padded = (g.p2_chunks + 7) / 8 * 8;
   // device-counted work: a grid of at most kPersist workgroups strides over it
-  constexpr int kPersist = 1024;
+  // (kPersistRows for the overflow points, usually none: an empty launch of
+  // the larger grid costs microseconds)
+  constexpr int kPersist = 1024, kPersistRows = 256;
   if (kmap != nullptr) {   // compacted components: one 16-component subtile per item
     const int items = g.Kp / 16 * padded;
     hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, true, true>), dim3(items < kPersist ? items : kPersist),
@@ -531,7 +533,7 @@ static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
   const int items = g.p2_kblocks * padded;
   if (ndyn != nullptr) {
     hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false, true>),
-                       dim3(items < kPersist ? items : kPersist), dim3(64 * kP2Waves), 0, s, X,
+                       dim3(items < kPersistRows ? items : kPersistRows), dim3(64 * kP2Waves), 0, s, X,
                        g.N, g.d, g.Kp, P, bias, ln2, part, g.p2_chunk, g.p2_chunks,
                        g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
     return hipGetLastError();

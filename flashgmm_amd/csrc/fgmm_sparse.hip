@@ -52,23 +52,35 @@ static_assert(kSpPts == kT, "one point per thread");
 constexpr int kAccUnroll = 4;      // entries per lane group in flight
 constexpr int kSpCountMax = 2048;  // up to this Kp the chunk sort is a counting sort
 constexpr int kPieceGrid = 2048;   // workgroups of the piece kernel (grid-stride)
+constexpr int kGroupGrid = 256;    // group fold: at least this many workgroups (grid-stride),
+                                   // one per 8 pieces of capacity up to kPieceGrid
 
-// exclusive scan over the workgroup (NT threads), one value per thread
+// exclusive scan over the workgroup (NT threads), one value per thread:
+// inclusive scan within each wavefront by shuffles, the wavefront totals
+// through LDS (sh holds at least NT / 64 ints), two barriers
 template <int NT>
 __device__ inline int block_excl_scan(int v, int* sh, int* total) {
-  const int tid = threadIdx.x;
-  sh[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < NT; off <<= 1) {
-    const int u = tid >= off ? sh[tid - off] : 0;
-    __syncthreads();
-    sh[tid] += u;
-    __syncthreads();
+  constexpr int NW = NT / 64;
+  static_assert(NT % 64 == 0 && NW <= 64, "whole wavefronts");
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(x, off, 64);
+    if (lane >= off) x += u;
   }
-  const int incl = sh[tid];
-  if (total != nullptr) *total = sh[NT - 1];
+  if (lane == 63) sh[w] = x;
   __syncthreads();
-  return incl - v;
+  int below = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < NW; i++) {
+    const int t = sh[i];
+    below += i < w ? t : 0;
+    all += t;
+  }
+  if (total != nullptr) *total = all;
+  __syncthreads();   // sh may be reused on return
+  return below + x - v;
 }
 
 // ---------------------------------------------------------------------------
@@ -596,7 +608,8 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   else e = piece_launch<32>(g, X, sp, s);
   if (e != hipSuccess) return e;
   const long cap = sp_npiece_cap(g);
-  hipLaunchKernelGGL(sp_group_kernel, dim3(cap < 2048 ? cap : 2048), dim3(kT), 0, s, g.d, g.dp,
+  const long gg = cap / 8 < kGroupGrid ? kGroupGrid : (cap / 8 > kPieceGrid ? kPieceGrid : cap / 8);
+  hipLaunchKernelGGL(sp_group_kernel, dim3(cap < gg ? cap : gg), dim3(kT), 0, s, g.d, g.dp,
                      g.stat_w, sp.pstart, sp.pcomp, sp.nov, sp.prow);
   return hipGetLastError();
 }
