@@ -128,8 +128,6 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   char* ln2o = take(sizeof(double) * N);
   char* kmap = take(sizeof(int) * Kp);
   char* nflag = take(sizeof(int));
-  char* Pf = take(sizeof(double) * 2 * Kp * (size_t)g.dp);
-  char* biasf = take(sizeof(double) * Kp);
   char* flag = take(sizeof(int) * Kp);
   char* dmass = take(sizeof(float) * (size_t)g.p1_blocks * Kp);
   if (b != nullptr) {
@@ -159,8 +157,6 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
     sp->ln2o = reinterpret_cast<double*>(ln2o);
     sp->kmap = reinterpret_cast<int*>(kmap);
     sp->nflag = reinterpret_cast<int*>(nflag);
-    sp->Pf = reinterpret_cast<double*>(Pf);
-    sp->biasf = reinterpret_cast<double*>(biasf);
   }
   return off;
 }
@@ -341,14 +337,11 @@ static int run_reduce(const Geom& g, const float* X, Ws& w, float* mu, float* va
     int rc = check_hip(launch_reduce_sparse(g, w.sp.prow, 1, w.part, w.sp.nov, g.p2_chunk,
                                             w.lnsum, mu, var, lp, params_next, bias_next,
                                             ll_out, s, kReduceFlagging, w.x.flag, w.sp.pstart,
-                                            w.x.dmass, w.sp.glob),
+                                            w.x.dmass, w.sp.glob, w.sp.kmap, w.sp.nflag),
                        "reduction / M-step");
     if (rc) return rc;
     // flagged components: all points, fp64 matrix cores, rows [s][k] of w.part
-    rc = check_hip(launch_flag_compact(g, w.x.flag, w.params, w.bias, w.sp, s),
-                   "flagged components (sparse)");
-    if (rc) return rc;
-    rc = check_hip(launch_pass2_mfma_map(g, X, w.sp.Pf, w.sp.biasf, w.ln2, w.part, w.sp.kmap,
+    rc = check_hip(launch_pass2_mfma_map(g, X, w.params, w.bias, w.ln2, w.part, w.sp.kmap,
                                          w.sp.nflag, s),
                    "exact statistics (sparse)");
     if (rc) return rc;

@@ -216,7 +216,8 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               int* __restrict__ flag, const double* __restrict__ part2,
                               const int* __restrict__ ndyn, long chunk2,
                               const int* __restrict__ pstart, const float* __restrict__ dmass,
-                              int nblk, const double* __restrict__ glob) {
+                              int nblk, const double* __restrict__ glob,
+                              int* __restrict__ kmap, int* __restrict__ nflag) {
   __shared__ double red[16];
   __shared__ double nk_sh;
   __shared__ double errb_sh[3];
@@ -369,7 +370,12 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   __syncthreads();
   if (stage == kReduceFlagging) {
     const bool bad = bad_sh != 0;
-    if (threadIdx.x == 0) flag[k] = bad ? 1 : 0;
+    if (threadIdx.x == 0) {
+      flag[k] = bad ? 1 : 0;
+      // sparse: the flagged components' list for the exact pass (slot order
+      // is free: a component's sums do not depend on its slot)
+      if (bad && kmap != nullptr) kmap[atomicAdd(nflag, 1)] = k;
+    }
     if (bad) return;   // statistics recomputed exactly, then reduced in stage 2
   }
   for (int j = threadIdx.x; j < d; j += blockDim.x) {
@@ -417,7 +423,7 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
                      bias_next, ll_out, standard, stage, flag, nullptr, nullptr, 1L, nullptr,
-                     nullptr, 0, nullptr);
+                     nullptr, 0, nullptr, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -426,17 +432,18 @@ hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const 
                                 float* new_mu, float* new_var, float* new_log_pi,
                                 double* params_next, double* bias_next, double* ll_out,
                                 hipStream_t s, int stage, int* flag, const int* pstart,
-                                const float* dmass, const double* glob) {
+                                const float* dmass, const double* glob, int* kmap, int* nflag) {
   if (g.variant != kSparse || stage == kReduceAll || flag == nullptr || S < 1 ||
       g.stat_w < 2 * g.dp + 4 || (part2 != nullptr && (ndyn == nullptr || chunk2 < 1)) ||
-      (pstart != nullptr && (dmass == nullptr || glob == nullptr)))
+      (pstart != nullptr && (dmass == nullptr || glob == nullptr)) ||
+      ((kmap == nullptr) != (nflag == nullptr)) || (kmap != nullptr && stage != kReduceFlagging))
     return hipErrorInvalidValue;
   const int blocks = (params_next != nullptr || stage == kReduceFlagging) ? g.Kp : g.K;
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(kReduceThreadsMax), 0, s, g.variant, g.N,
                      g.K, g.Kp, g.d, g.dp, S, g.stat_w, part, lnsum, g.p1_blocks, nullptr,
                      nullptr, nullptr, new_mu, new_var, new_log_pi, params_next, bias_next,
                      ll_out, 0, stage, flag, part2, ndyn, chunk2 < 1 ? 1L : chunk2, pstart,
-                     dmass, g.p1_blocks, glob);
+                     dmass, g.p1_blocks, glob, kmap, nflag);
   return hipGetLastError();
 }
 

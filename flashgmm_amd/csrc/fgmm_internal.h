@@ -138,10 +138,8 @@ struct SpWs {
   double* prow;        // [npiece_cap][stat_w] piece sums
   float* Xo;           // [N][d] rows of the overflow points
   double* ln2o;        // [N] their log-normalizers
-  int* kmap;           // [Kp] flagged components, compacted (-1 = padding)
+  int* kmap;           // [Kp] flagged components, any order (-1 = padding)
   int* nflag;          // [1]
-  double* Pf;          // fp64 fragment coefficients of the flagged components
-  double* biasf;       // [Kp]
 };
 // Piece rows: a fixed budget; the device widens the pieces past kSpPiece
 // entries when the lists hold more than kSpPiece x budget entries.
@@ -244,28 +242,28 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
 // rows pstart[k] .. pstart[k+1] of part, plus the never-pending bounds dmass
 // and glob in the error columns), then the first ceil(*ndyn / chunk2) rows of
 // part2 (the dense pass over the overflow points; none if part2 is null).
-// Error-bound columns come from part alone.
+// Error-bound columns come from part alone.  In stage kReduceFlagging, kmap /
+// nflag (cleared by the sparse Pass 2) receive the flagged components.
 hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const double* part2,
                                 const int* ndyn, long chunk2, const double* lnsum,
                                 float* new_mu, float* new_var, float* new_log_pi,
                                 double* params_next, double* bias_next, double* ll_out,
                                 hipStream_t s, int stage, int* flag, const int* pstart = nullptr,
-                                const float* dmass = nullptr, const double* glob = nullptr);
+                                const float* dmass = nullptr, const double* glob = nullptr,
+                                int* kmap = nullptr, int* nflag = nullptr);
 // Sparse Pass 2: chunk sort, scans, placement (+ gather of the overflow
-// points), piece sums (sp.prow, reduced per component by the reduction).
+// points), piece sums (sp.prow, reduced per component by the reduction);
+// clears the flagged-component list (sp.kmap = -1, sp.nflag = 0).
 hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, const SpWs& sp,
                                const double* ln2, hipStream_t s);
-// Flagged components (flag[k] != 0) compacted into sp.kmap / sp.nflag with
-// their fp64 fragment coefficients gathered into sp.Pf / sp.biasf.
-hipError_t launch_flag_compact(const Geom& g, const int* flag, const double* P,
-                               const double* bias, const SpWs& sp, hipStream_t s);
 // fp64 matrix-core Pass 2 over the first *ndyn rows of X (device count, at
 // most g.N); chunks past them exit without writing.
 hipError_t launch_pass2_mfma_dyn(const Geom& g, const float* X, const double* P,
                                  const double* bias, const double* ln2, double* part,
                                  const int* ndyn, hipStream_t s);
-// fp64 matrix-core Pass 2 over all points for the compacted components of
-// P/bias (the first *kdyn of them); the row of compact component i is
+// fp64 matrix-core Pass 2 over all points for the listed components kmap[i],
+// i < *kdyn (-1 beyond, up to a multiple of 16), their coefficients gathered
+// from the fragment-ordered P / bias; the row of listed component i is
 // part[s][kmap[i]].
 hipError_t launch_pass2_mfma_map(const Geom& g, const float* X, const double* P,
                                  const double* bias, const double* ln2, double* part,

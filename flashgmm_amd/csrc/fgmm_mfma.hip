@@ -270,7 +270,13 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
 
   double pr[S1];
   double bk = -INFINITY;
-  if (active) {
+  if (active && kmap != nullptr) {   // listed components, gathered from P
+    const int kk = kmap[ks * 16 + c];
+#pragma unroll
+    for (int s = 0; s < S1; s++)
+      pr[s] = kk >= 0 ? P[((size_t)(kk >> 4) * S1 + s) * 64 + 16 * g + (kk & 15)] : 0.0;
+    bk = kk >= 0 ? bias[kk] : -INFINITY;
+  } else if (active) {
 #pragma unroll
     for (int s = 0; s < S1; s++) pr[s] = P[((size_t)ks * S1 + s) * 64 + lane];
     bk = bias[ks * 16 + c];

@@ -31,7 +31,6 @@
 //   sp_piece_kernel   fp64 sums over one piece per workgroup
 //   sp_group_kernel   components with more than 64 pieces: groups of rows
 //                     summed in order; the reduction sums the rest in order
-//   sp_flag_kernel    flagged components -> compact list and coefficients
 //
 // Reference kernel this replaces (file:line in the reference repository):
 //   Pass 2  flash_accumulate_stats_v2_kernel  flash_gmm/csrc/flash_gmm_cuda.cu:179-292
@@ -257,7 +256,8 @@ __global__ __launch_bounds__(kT) void sp_rowscan_kernel(int Kp, int nchunk, int*
 __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
     long N, int Kp, int nchunk, long budget, const int* __restrict__ rowtot, int* __restrict__ ocnt,
     const double* __restrict__ xsum, int* __restrict__ seg, int* __restrict__ pstart,
-    int* __restrict__ pcomp, int* __restrict__ nov, double* __restrict__ glob) {
+    int* __restrict__ pcomp, int* __restrict__ nov, double* __restrict__ glob,
+    int* __restrict__ kmap, int* __restrict__ nflag) {
   __shared__ int sh[kScanThreads];
   __shared__ double d1[kScanThreads / 64];
   extern __shared__ int ps[];   // [Kp + 1] first piece of each component
@@ -289,7 +289,10 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
     }
     pcarry += ptot;
   }
+  // empty flagged-component list, filled by the reduction's first stage
+  for (int k = tid; k < Kp; k += kScanThreads) kmap[k] = -1;
   if (tid == 0) {
+    nflag[0] = 0;
     seg[Kp] = carry;
     pstart[Kp] = pcarry;
     ps[Kp] = pcarry;
@@ -508,50 +511,6 @@ __global__ __launch_bounds__(kT) void sp_group_kernel(int d, int dp, int stat_w,
   }
 }
 
-// ---------------------------------------------------------------------------
-// flagged components: compact list + gathered fp64 fragment coefficients
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kScanThreads) void sp_flag_kernel(
-    int K, int Kp, int dp, const int* __restrict__ flag, const double* __restrict__ P,
-    const double* __restrict__ bias, int* __restrict__ kmap, int* __restrict__ nflag,
-    double* __restrict__ Pf, double* __restrict__ biasf) {
-  __shared__ int sh[kScanThreads];
-  __shared__ int nf_sh;
-  const int tid = threadIdx.x;
-  int carry = 0;
-  for (int b = 0; b < Kp; b += kScanThreads) {
-    const int k = b + tid;
-    const int v = (k < K && flag[k] != 0) ? 1 : 0;
-    int tot;
-    const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
-    if (v) kmap[carry + ex] = k;
-    carry += tot;
-  }
-  if (tid == 0) nf_sh = carry;
-  __syncthreads();
-  const int nf = nf_sh;
-  const int n16 = (nf + 15) & ~15;
-  for (int i = nf + tid; i < n16; i += kScanThreads) kmap[i] = -1;
-  if (tid == 0) nflag[0] = nf;
-  __syncthreads();
-  // fragment layout: P[((ks * S1 + t) * 64 + 16 g + c] for component 16 ks + c
-  const int S1 = dp / 2;
-  const long per = (long)S1 * 4;
-  for (long idx = tid; idx < (long)n16 * per; idx += kScanThreads) {
-    const int i = (int)(idx / per);
-    const int r = (int)(idx - (long)i * per);
-    const int t = r >> 2, g = r & 3;
-    const int k = kmap[i];
-    const double v =
-        k >= 0 ? P[((size_t)(k >> 4) * S1 + t) * 64 + 16 * g + (k & 15)] : 0.0;
-    Pf[((size_t)(i >> 4) * S1 + t) * 64 + 16 * g + (i & 15)] = v;
-  }
-  for (int i = tid; i < n16; i += kScanThreads) {
-    const int k = kmap[i];
-    biasf[i] = k >= 0 ? bias[k] : -INFINITY;
-  }
-}
-
 template <int L>
 hipError_t piece_launch(const Geom& g, const float* X, const SpWs& sp, hipStream_t s) {
   const long cap = sp_npiece_cap(g);
@@ -596,7 +555,8 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(sp_top_kernel, dim3(1), dim3(kScanThreads), sizeof(int) * (g.Kp + 1), s,
                      g.N, g.Kp, g.sp_nchunk,
-                     sp_piece_budget(g), sp.rowtot, sp.ocnt, sp.xsum, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.glob);
+                     sp_piece_budget(g), sp.rowtot, sp.ocnt, sp.xsum, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.glob,
+                     sp.kmap, sp.nflag);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(sp_place_kernel, dim3(g.sp_nchunk), dim3(kT), sizeof(int) * (size_t)g.Kp,
                      s, g.N, g.d, g.Kp, g.sp_C, g.sp_nchunk, sp.blk, sp.ecnt, sp.fcap, sp.seg,
@@ -611,14 +571,6 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   const long gg = cap / 8 < kGroupGrid ? kGroupGrid : (cap / 8 > kPieceGrid ? kPieceGrid : cap / 8);
   hipLaunchKernelGGL(sp_group_kernel, dim3(cap < gg ? cap : gg), dim3(kT), 0, s, g.d, g.dp,
                      g.stat_w, sp.pstart, sp.pcomp, sp.nov, sp.prow);
-  return hipGetLastError();
-}
-
-hipError_t launch_flag_compact(const Geom& g, const int* flag, const double* P,
-                               const double* bias, const SpWs& sp, hipStream_t s) {
-  if (g.variant != kSparse) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sp_flag_kernel, dim3(1), dim3(kScanThreads), 0, s, g.K, g.Kp, g.dp, flag,
-                     P, bias, sp.kmap, sp.nflag, sp.Pf, sp.biasf);
   return hipGetLastError();
 }
 
