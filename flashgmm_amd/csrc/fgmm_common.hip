@@ -93,15 +93,15 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
     }
     if (sp) {
       // octet order: lane group g holds features 32u + 8g + v (v < 8) as its
-      // t-th feature, t = 8u + v.  Exact-evaluation rows, 12 bytes per
-      // feature in 16-byte groups: s (fp64) [Kp][dpb], lane g's features
-      // t, t+1 (t even) as one double2 at position 4 (t/2) + g; then mu (the
-      // fp32 parameter itself) [Kp][dpb], features t .. t+3 (t = 0 mod 4) as
-      // one float4 at position 4 (t/4) + g.
+      // t-th feature, t = 8u + v.  Exact-evaluation rows, 8 bytes per
+      // feature: var (the fp32 parameter itself; 1 for padding) [Kp][dpb],
+      // then mu (fp32) [Kp][dpb]; lane g's features t .. t+3 (t = 0 mod 4) as
+      // one float4 at position 4 (t/4) + g of the row.
       const int gg = (j & 31) >> 3, tt = 8 * (j >> 5) + (j & 7);
-      Vx[(size_t)k * dpb + ((tt >> 1) * 4 + gg) * 2 + (tt & 1)] = sqrt(0.5 * kLog2e * iv);
-      reinterpret_cast<float*>(Vx + (size_t)Kp * dpb)[(size_t)k * dpb + ((tt >> 2) * 4 + gg) * 4 + (tt & 3)] =
-          (float)mu;
+      const size_t fi = (size_t)k * dpb + ((tt >> 2) * 4 + gg) * 4 + (tt & 3);
+      float* Vf = reinterpret_cast<float*>(Vx);
+      Vf[fi] = (real && j < d) ? v[j] : 1.0f;
+      Vf[(size_t)Kp * dpb + fi] = (float)mu;
       // bf16 fragments [ks][step][hi, lo][lane][8]: step s < dpb/32 holds the
       // x^2 coefficients of features 32s .. 32s+31, step dpb/32 + s the x ones;
       // lane 16 g' + c holds features 32s + 8g' .. +7 of component 16 ks + c

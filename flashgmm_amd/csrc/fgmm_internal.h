@@ -76,7 +76,7 @@ struct WsLayout {
 
 // Coefficient views of the x32 variant (see fgmm_x32.hip).  The params
 // region holds the fp64 direct-form coefficients V2 ((s_kj, mu_kj s_kj)
-// pairs, quarter-interleaved, see x32_dist; the sparse variant: s_kj fp64
+// pairs, quarter-interleaved, see x32_dist; the sparse variant: var_kj fp32
 // [Kp][dpb] then mu_kj fp32 [Kp][dpb], in 16-byte groups per lane, see
 // write_coeffs) followed by the fp32 fragment-ordered
 // coefficients; the bias region holds the fp64 direct-form bias, the fp32

@@ -285,21 +285,20 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
       const int a_ = ix_ * kThr1 + wave * 64 + gs_ * 16 + p_;                         \
       const int k_ = plist[a_].x;                                                     \
       double q_ = 0.0;                                                                \
-      if (BF) {   /* (s fp64, mu fp32) rows: t = (x - mu) s, x - mu exact */            \
-        const double2* cs_ = reinterpret_cast<const double2*>(V2) + (size_t)k_ * (DPB / 2) + g; \
-        const float4* cm_ =                                                           \
-            reinterpret_cast<const float4*>(V2 + (size_t)Kp * DPB) + (size_t)k_ * (DPB / 4) + g; \
+      if (BF) {   /* (var, mu) fp32 rows: (x - mu)^2 / var in fp64, x - mu exact */    \
+        const float4* cv_ = reinterpret_cast<const float4*>(V2) + (size_t)k_ * (DPB / 4) + g; \
+        const float4* cm_ = cv_ + (size_t)Kp * (DPB / 4);                             \
         _Pragma("unroll") for (int w_ = 0; w_ < QX / 4; w_++) {                       \
-          const float4 m_ = cm_[4 * w_];                                              \
-          const double2 sa_ = cs_[8 * w_], sb_ = cs_[8 * w_ + 4];                     \
+          const float4 m_ = cm_[4 * w_], v4_ = cv_[4 * w_];                           \
           const float mv_[4] = {m_.x, m_.y, m_.z, m_.w};                              \
-          const double sv_[4] = {sa_.x, sa_.y, sb_.x, sb_.y};                         \
+          const float vv_[4] = {v4_.x, v4_.y, v4_.z, v4_.w};                          \
           _Pragma("unroll") for (int i4_ = 0; i4_ < 4; i4_++) {                       \
             const float xv_ = __shfl(xq[4 * w_ + i4_], p_, 16);                       \
-            const double t_ = ((double)xv_ - (double)mv_[i4_]) * sv_[i4_];            \
-            q_ = fma(t_, t_, q_);                                                     \
+            const double t_ = (double)xv_ - (double)mv_[i4_];                         \
+            q_ += t_ * t_ / (double)vv_[i4_];                                         \
           }                                                                           \
         }                                                                             \
+        q_ *= 0.5 * kLog2e;                                                           \
       } else {                                                                        \
         const double2* cf_ = reinterpret_cast<const double2*>(V2) + (size_t)k_ * VROW + g; \
         _Pragma("unroll") for (int j_ = 0; j_ < QX; j_++) {                           \
