@@ -34,10 +34,11 @@ static int fail(int code, const char* fmt, ...) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Variant table keyed by (K, d).  Matrix cores need >= 16 components to fill
-// a 16x16 tile (K is padded to 32) and hold the 16-component coefficient
-// fragment in registers up to d = 128; below or above that the vector-ALU
-// kernels run.
+// Variant table keyed by (K, d).  The matrix-core kernels pad K to 32 and
+// hold the 16-component coefficient fragment in registers up to d = 128;
+// from K = 8 they beat the vector-ALU kernels despite the padding (1.2x to
+// 2.3x measured for K = 8 .. 15, N = 2^12 .. 2^20), below that the
+// padding costs more than the matrix cores save (0.7x at K = 4, N = 2^20).
 // From K >= 128 the sparse variant (x32 Pass 1 listing each point's exact
 // pairs, statistics from those lists) beats the dense fp64 Pass 2 by
 // 1.1x (K = 128) to 2.5x (K = 512, N = 2^20) at d = 64 and 128 (measured);
@@ -47,7 +48,7 @@ static int resolve_variant(long N, int K, int d, int variant) {
   if (d <= 128 && K >= 128 && K <= 8192 && N * (long)(K < kSpCap ? K : kSpCap) < 2147483647L)
     return kSparse;
   if (d <= 128 && K >= 256) return kMixed;
-  if (d <= 128 && K >= 16) return kMfma;
+  if (d <= 128 && K >= 8) return kMfma;
   return kValu;
 }
 

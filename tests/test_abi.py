@@ -47,16 +47,17 @@ def test_python_signatures_cover_header():
 
 def test_version_and_variant_table(lib):
     assert lib.fgmm_version() >= 100
-    # matrix cores from K >= 16 and d <= 128 (with the x32 log-normalizer
+    # matrix cores from K >= 8 and d <= 128 (with the x32 log-normalizer
     # pass from K >= 256), vector ALU otherwise
     assert lib.fgmm_resolve_variant(65536, 256, 128, 0) == 5
     assert lib.fgmm_resolve_variant(262144, 128, 64, 0) == 5
     assert lib.fgmm_resolve_variant(4096, 64, 32, 0) == 2
     assert lib.fgmm_resolve_variant(65536, 9000, 64, 0) == 4        # K > 8192: mixed
     assert lib.fgmm_resolve_variant(1 << 27, 256, 64, 0) == 4       # N * 32 >= 2^31
-    assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 1
+    assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 2
+    assert lib.fgmm_resolve_variant(4096, 7, 32, 0) == 1
     assert lib.fgmm_resolve_variant(4096, 64, 200, 0) == 1
-    assert lib.fgmm_resolve_variant(4096, 8, 32, 2) == 2
+    assert lib.fgmm_resolve_variant(4096, 8, 32, 1) == 1          # forced vector ALU
 
 
 def test_workspace_bytes(lib):
@@ -75,7 +76,7 @@ def test_workspace_bytes(lib):
 def test_estep_workspace_bytes(lib):
     for N, K, d in ((4096, 8, 32), (65536, 256, 128), (5, 3, 256), (1, 1, 1)):
         # the E-steps run the fp64 matrix-core (or vector) layout
-        base = lib.fgmm_workspace_bytes(N, K, d, 2 if (d <= 128 and K >= 16) else 1)
+        base = lib.fgmm_workspace_bytes(N, K, d, 2 if (d <= 128 and K >= 8) else 1)
         std = lib.fgmm_standard_e_step_workspace_bytes(N, K, d, 0)
         assert std % 256 == 0 and std >= base + 8 * N * K   # + the fp64 N x K matrix
         # x32 has no gamma-returning form: it runs as the MFMA path
