@@ -84,6 +84,19 @@ FP32_SWEEP = ("x32", "mixed")   # Pass 1 on fp32 matrix cores
 BF16_SWEEP = ("sparse",)        # Pass 1 on bf16 matrix cores, operands split hi + lo
 
 
+def arithmetic_type(variant: str) -> str:
+    """What the variant computes in (inputs and outputs are fp32 throughout)."""
+    if variant in BF16_SWEEP:
+        return ("f64 (pairs near each point's maximum, statistics, reduction) + "
+                "bf16x3 matrix-core bound sweep with fp32 accumulation")
+    if variant == "x32":
+        return "f32 matrix-core sweeps with error bounds + f64 window pairs and reduction"
+    if variant in ("mfma", "mixed"):
+        return ("f64 matrix cores (distance, sum gamma x^2, reduction) + f32 (gamma, sum gamma x)"
+                + (" + f32 matrix-core Pass-1 bound sweep" if variant == "mixed" else ""))
+    return "f64 (vector ALU)"
+
+
 def dominant_roofline(cfg, variant, kernels):
     """Roofline of the kernel that takes the most time per iteration.
 
@@ -283,7 +296,7 @@ def line_for(cid, args, with_cpu):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 (distance contraction in f64)",
+        "dtype": arithmetic_type(r["variant"]),
         "data": "synthetic (seeded mixture generator, flashgmm_amd/configs.py)",
         "config": {"workload": f"C{cid}: diag-cov GMM EM N={cfg.N} K={cfg.K} d={cfg.d} fp32",
                    "N": cfg.N, "K": cfg.K, "d": cfg.d, "kernel_variant": r["variant"]},
