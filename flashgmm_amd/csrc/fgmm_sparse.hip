@@ -407,14 +407,23 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
     const int e1 = min(e0 + piece, seg[k + 1]);
     double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
     double nk = 0.0, eb = 0.0, es = 0.0, eq = 0.0;
-    for (int e = e0 + h; e < e1; e += H * kAccUnroll) {
-      int2 en[kAccUnroll];
-      float4 xv[kAccUnroll];
+    // entries of the next batch are loaded while this batch's rows of X are
+    // in flight (weight 0 past the piece: no effect)
+    constexpr int kStep = H * kAccUnroll;
+    int2 en[kAccUnroll];
+#pragma unroll
+    for (int u = 0; u < kAccUnroll; u++) {
+      const int eu = e0 + h + u * H;
+      en[u] = eu < e1 ? sorted[eu] : make_int2(0, 0);
+    }
+    for (int e = e0 + h; e < e1; e += kStep) {
+      int2 nx[kAccUnroll];
 #pragma unroll
       for (int u = 0; u < kAccUnroll; u++) {
-        const int eu = e + u * H;
-        en[u] = eu < e1 ? sorted[eu] : make_int2(0, 0);   // weight 0: no effect
+        const int eu = e + kStep + u * H;
+        nx[u] = eu < e1 ? sorted[eu] : make_int2(0, 0);
       }
+      float4 xv[kAccUnroll];
 #pragma unroll
       for (int u = 0; u < kAccUnroll; u++) {
         xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -452,6 +461,8 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
         }
         nk += w;
       }
+#pragma unroll
+      for (int u = 0; u < kAccUnroll; u++) en[u] = nx[u];
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
