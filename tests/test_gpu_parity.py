@@ -291,6 +291,34 @@ def test_x32_starved_component_takes_exact_path(cuda):
         check_params(out[:3], ref, f"starved {variant}")
 
 
+def test_many_starved_components_flagged(cuda):
+    """Forty clones of one component, each weighted 2^-41 below it: every
+    clone is starved (its mass lies just outside the exact window), so the
+    error bounds flag all forty.  The flagged list then spans three
+    16-component subtiles of the exact pass, and the result must still match
+    the fp64 oracle for every component."""
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(11)
+    N, d, base, clones = 20000, 64, 4, 40
+    centers = rng.uniform(-4, 4, (base, d))
+    labels = rng.integers(0, base, N)
+    X = (centers[labels] + rng.normal(0, 1, (N, d))).astype(np.float32)
+    K = base + clones
+    mu = np.concatenate([centers, np.repeat(centers[:1], clones, 0)]).astype(np.float32)
+    var = np.ones((K, d), np.float32)
+    lp = np.full(K, -np.log(base), np.float32)
+    lp[base:] = lp[0] - 41 * np.log(2.0)
+    _, _, _, ln, (n_k, s_k, sq_k) = O.c_em_fused(X, mu, var, lp, with_stats=True)
+    ref = O.c_m_step_update(n_k, s_k, sq_k, N)
+    assert (n_k[base:] < 1e-7).all(), n_k[base:].max()   # every clone starved
+    t = to_dev(cuda, X, mu, var, lp)
+    for variant in ("sparse", "mixed", "x32"):
+        print(f"[case] {clones} starved clones variant={variant}", flush=True)
+        out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
+        check_ln(out[3], ln, f"many starved {variant}")
+        check_params(out[:3], ref, f"many starved {variant}")
+
+
 def test_x32_crowded_window_overflows_slots(cuda):
     """64 nearly identical components: every point has ~64 pairs inside the
     exact window, far more than its 16 slots, so Pass 2 recomputes the
