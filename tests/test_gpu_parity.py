@@ -194,6 +194,8 @@ EDGE = {
     "d256": dict(N=300, K=5, d=256),
     "d130": dict(N=100, K=20, d=130),
     "K33_N1025": dict(N=1025, K=33, d=64),
+    # Kp > 2048: the sparse chunk sort takes its bitonic path
+    "K3000": dict(N=4096, K=3000, d=32),
 }
 
 
