@@ -53,6 +53,27 @@ __device__ inline double block_sum_f64(double v, double* red) {
   return t;
 }
 
+// NV block sums at once (red holds NV doubles per wavefront); each value is
+// summed exactly as block_sum_f64 sums it, with two barriers in all.
+template <int NV>
+__device__ inline void block_sum_f64_n(double (&v)[NV], double* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int j = 0; j < NV; j++) v[j] = wave_sum_f64(v[j]);
+  __syncthreads();
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < NV; j++) red[w * NV + j] = v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    double t = 0.0;
+    for (int i = 0; i < nw; i++) t += red[i * NV + j];
+    v[j] = t;
+  }
+}
+
 // Writes the coefficients of component k (block-cooperative over j).
 // m / v are the fp32 parameter values of this component (nullptr for a
 // padding component, which gets zero coefficients and bias -inf).
@@ -134,8 +155,12 @@ __device__ void write_coeffs(int variant, int k, int Kp, int d, int dp,
       P32[((size_t)ks * S1 + Q + t) * 64 + lane] = (float)(kLog2e * mu * iv);
     }
   }
-  lnv = block_sum_f64(lnv, red);
-  q = block_sum_f64(q, red);
+  {
+    double lq[2] = {lnv, q};   // red holds 2 per wavefront: blockDim <= 512
+    block_sum_f64_n<2>(lq, red);
+    lnv = lq[0];
+    q = lq[1];
+  }
   if (threadIdx.x == 0) {
     float* bias32 = reinterpret_cast<float*>(bx + Kp);
     float* Z32 = bias32 + Kp;
@@ -219,6 +244,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               int nblk, const double* __restrict__ glob,
                               int* __restrict__ kmap, int* __restrict__ nflag) {
   __shared__ double red[16];
+  __shared__ double redn[5 * 16];   // five block sums at once (up to 16 wavefronts)
   __shared__ double nk_sh;
   __shared__ double errb_sh[3];
   __shared__ int bad_sh;
@@ -269,27 +295,31 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
       const double* p2 = part2 + (size_t)k * row + 2 * dp;
       for (int s = threadIdx.x; s < S2; s += blockDim.x) t += p2[(size_t)s * kstride];
     }
-    t = block_sum_f64(t, red);
     if (stage == kReduceFlagging) {
-      for (int c = 1; c <= 3; c++) {
-        double e = 0.0;
-        for (int s = threadIdx.x; s < Sk; s += blockDim.x) e += p[(size_t)s * kst + c];
-        e = block_sum_f64(e, red);
-        if (threadIdx.x == 0) errb_sh[c - 1] = e;
-      }
-      if (dmass != nullptr) {
-        // sparse: pairs that never became pending (Pass-1 workgroup bounds, in
-        // order), weighted by the global max |x| / x^2, plus the floor
-        double e = 0.0;
-        for (int b = threadIdx.x; b < nblk; b += blockDim.x) e += (double)dmass[(size_t)k * nblk + b];
-        e = block_sum_f64(e, red);
-        if (threadIdx.x == 0) {
-          const double dk = e * (1.0 + 0x1p-40) + glob[0];
+      // n_k, the three error columns and (sparse) the never-pending bounds,
+      // reduced together
+      double v5[5] = {t, 0.0, 0.0, 0.0, 0.0};
+      for (int c = 1; c <= 3; c++)
+        for (int s = threadIdx.x; s < Sk; s += blockDim.x) v5[c] += p[(size_t)s * kst + c];
+      if (dmass != nullptr)
+        for (int b = threadIdx.x; b < nblk; b += blockDim.x) v5[4] += (double)dmass[(size_t)k * nblk + b];
+      block_sum_f64_n<5>(v5, redn);
+      t = v5[0];
+      if (threadIdx.x == 0) {
+        errb_sh[0] = v5[1];
+        errb_sh[1] = v5[2];
+        errb_sh[2] = v5[3];
+        if (dmass != nullptr) {
+          // sparse: pairs that never became pending (Pass-1 workgroup bounds,
+          // in order), weighted by the global max |x| / x^2, plus the floor
+          const double dk = v5[4] * (1.0 + 0x1p-40) + glob[0];
           errb_sh[0] += dk;
           errb_sh[1] += dk * glob[1];
           errb_sh[2] += dk * glob[2];
         }
       }
+    } else {
+      t = block_sum_f64(t, red);
     }
     if (threadIdx.x == 0) {
       nk_sh = t;
