@@ -120,7 +120,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   char* xsum = take(sizeof(double) * nch);
   char* seg = take(sizeof(int) * (Kp + 1));
   char* pstart = take(sizeof(int) * (Kp + 1));
-  char* pcomp = take(sizeof(int) * npc);
+  char* pinfo = take(sizeof(int4) * npc);
   char* nov = take(sizeof(int) * 3);
   char* glob = take(sizeof(double) * 4);
   char* sorted = take(sizeof(int2) * NC);
@@ -149,7 +149,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
     sp->xsum = reinterpret_cast<double*>(xsum);
     sp->seg = reinterpret_cast<int*>(seg);
     sp->pstart = reinterpret_cast<int*>(pstart);
-    sp->pcomp = reinterpret_cast<int*>(pcomp);
+    sp->pinfo = reinterpret_cast<int4*>(pinfo);
     sp->nov = reinterpret_cast<int*>(nov);
     sp->glob = reinterpret_cast<double*>(glob);
     sp->sorted = reinterpret_cast<int2*>(sorted);

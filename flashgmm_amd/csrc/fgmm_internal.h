@@ -131,7 +131,8 @@ struct SpWs {
   double* xsum;        // [nchunk] max xm over the chunk
   int* seg;            // [Kp + 1] start of each component's entries
   int* pstart;         // [Kp + 1] first accumulation piece of each component
-  int* pcomp;          // [npiece_cap] component of each piece
+  int4* pinfo;         // [npiece_cap] per piece: entries [x, y), rows folded into it
+                       // (z >= 2 heads a group of z rows), component w
   int* nov;            // [3] overflow points, pieces, entries per piece
   double* glob;        // [4] N 2^-126 (with margin), max_n max_j |x_nj|, its square
   int2* sorted;        // [N * C] (point, float gamma bits) by (component, point)

@@ -256,11 +256,12 @@ __global__ __launch_bounds__(kT) void sp_rowscan_kernel(int Kp, int nchunk, int*
 __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
     long N, int Kp, int nchunk, long budget, const int* __restrict__ rowtot, int* __restrict__ ocnt,
     const double* __restrict__ xsum, int* __restrict__ seg, int* __restrict__ pstart,
-    int* __restrict__ pcomp, int* __restrict__ nov, double* __restrict__ glob,
+    int4* __restrict__ pinfo, int* __restrict__ nov, double* __restrict__ glob,
     int* __restrict__ kmap, int* __restrict__ nflag) {
   __shared__ int sh[kScanThreads];
   __shared__ double d1[kScanThreads / 64];
   extern __shared__ int ps[];   // [Kp + 1] first piece of each component
+  int* sg = ps + (Kp + 1);      // [Kp + 1] first entry of each component
   const int tid = threadIdx.x;
   int carry = 0;
   for (int b = 0; b < Kp; b += kScanThreads) {
@@ -268,7 +269,10 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
     const int len = k < Kp ? rowtot[k] : 0;
     int tot;
     const int ex = block_excl_scan<kScanThreads>(len, sh, &tot);
-    if (k < Kp) seg[k] = carry + ex;
+    if (k < Kp) {
+      seg[k] = carry + ex;
+      sg[k] = carry + ex;
+    }
     carry += tot;
   }
   // piece length: kSpPiece, or more when the piece rows would pass the budget
@@ -294,13 +298,16 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
   if (tid == 0) {
     nflag[0] = 0;
     seg[Kp] = carry;
+    sg[Kp] = carry;
     pstart[Kp] = pcarry;
     ps[Kp] = pcarry;
     nov[1] = pcarry;
     nov[2] = piece;
   }
   __syncthreads();
-  // component of each piece: the last k with ps[k] <= piece index
+  // component of each piece (the last k with ps[k] <= piece index), its
+  // entries, and for a component of more than kSpFoldRows pieces the rows
+  // that the group fold sums into the first row of each group of G
   for (int pc = tid; pc < pcarry; pc += kScanThreads) {
     int lo = 0, hi = Kp;   // ps[lo] <= pc < ps[hi]
     while (hi - lo > 1) {
@@ -308,7 +315,11 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
       if (ps[mid] <= pc) lo = mid;
       else hi = mid;
     }
-    pcomp[pc] = lo;
+    const int np = ps[lo + 1] - ps[lo], i = pc - ps[lo];
+    const int G = np > kSpFoldRows ? (np + kSpFoldRows - 1) / kSpFoldRows : 1;
+    const int e0 = sg[lo] + i * piece;
+    pinfo[pc] = make_int4(e0, min(e0 + piece, sg[lo + 1]),
+                          (G > 1 && i % G == 0) ? min(G, np - i) : 0, lo);
   }
   carry = 0;
   for (int b = 0; b < nchunk; b += kScanThreads) {
@@ -391,8 +402,8 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
 // ---------------------------------------------------------------------------
 template <int L, bool VEC>
 __global__ __launch_bounds__(kT) void sp_piece_kernel(
-    int d, int dp, int stat_w, const int* __restrict__ seg, const int* __restrict__ pstart,
-    const int* __restrict__ pcomp, const int* __restrict__ nov, const int2* __restrict__ sorted,
+    int d, int dp, int stat_w, const int4* __restrict__ pinfo, const int* __restrict__ nov,
+    const int2* __restrict__ sorted,
     const float* __restrict__ X, const float* __restrict__ xm, double* __restrict__ prow) {
   constexpr int H = kT / L;
   __shared__ double sa[H][4 * L], sb[H][4 * L];
@@ -400,11 +411,15 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
   const int tid = threadIdx.x;
   const int j = tid % L, h = tid / L;
   const int j0 = 4 * j;
-  const int npiece = nov[1], piece = nov[2];
+  const int npiece = nov[1];
+  // the piece's entry range, loaded one piece ahead (grid <= capacity: the
+  // first load is in bounds, and unused past npiece)
+  int4 cur = pinfo[blockIdx.x];
   for (int pc = blockIdx.x; pc < npiece; pc += gridDim.x) {
-    const int k = pcomp[pc];
-    const int e0 = seg[k] + (pc - pstart[k]) * piece;
-    const int e1 = min(e0 + piece, seg[k + 1]);
+    const int pn = pc + (int)gridDim.x;
+    const int4 nxp = pn < npiece ? pinfo[pn] : make_int4(0, 0, 0, 0);
+    const int e0 = cur.x, e1 = cur.y;
+    cur = nxp;
     double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
     double nk = 0.0, eb = 0.0, es = 0.0, eq = 0.0;
     // entries of the next batch are loaded while this batch's rows of X are
@@ -499,19 +514,13 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
 // ceil(pieces / kSpFoldRows), each group's sum (in order) written into its
 // first row, so the reduction reads at most kSpFoldRows rows per component.
 __global__ __launch_bounds__(kT) void sp_group_kernel(int d, int dp, int stat_w,
-                                                      const int* __restrict__ pstart,
-                                                      const int* __restrict__ pcomp,
+                                                      const int4* __restrict__ pinfo,
                                                       const int* __restrict__ nov,
                                                       double* __restrict__ prow) {
   const int npiece = nov[1];
   for (int r = blockIdx.x; r < npiece; r += gridDim.x) {
-    const int k = pcomp[r];
-    const int r0 = pstart[k], np = pstart[k + 1] - r0;
-    if (np <= kSpFoldRows) continue;
-    const int G = (np + kSpFoldRows - 1) / kSpFoldRows;
-    const int i = r - r0;
-    if (i % G != 0) continue;
-    const int n = min(G, np - i);
+    const int n = pinfo[r].z;   // rows of the group this row heads (0: none)
+    if (n < 2) continue;
     double* out = prow + (size_t)r * stat_w;
     for (int f = threadIdx.x; f < 2 * dp + 4; f += kT) {
       if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
@@ -528,10 +537,10 @@ hipError_t piece_launch(const Geom& g, const float* X, const SpWs& sp, hipStream
   const int grid = (int)(cap < kPieceGrid ? cap : kPieceGrid);
   if ((g.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0))
     hipLaunchKernelGGL((sp_piece_kernel<L, true>), dim3(grid), dim3(kT), 0, s, g.d, g.dp,
-                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.xm, sp.prow);
+                       g.stat_w, sp.pinfo, sp.nov, sp.sorted, X, sp.xm, sp.prow);
   else
     hipLaunchKernelGGL((sp_piece_kernel<L, false>), dim3(grid), dim3(kT), 0, s, g.d, g.dp,
-                       g.stat_w, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.sorted, X, sp.xm, sp.prow);
+                       g.stat_w, sp.pinfo, sp.nov, sp.sorted, X, sp.xm, sp.prow);
   return hipGetLastError();
 }
 
@@ -554,6 +563,10 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
         (const void*)sp_sort_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
         (int)((2 * (size_t)kSpChunkCap + 8192) * sizeof(int) + 36 * (size_t)kSpCountMax));
     if (e != hipSuccess) return e;
+    // top-level scan: first piece and first entry of each of up to 8192 components
+    e = hipFuncSetAttribute((const void*)sp_top_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(2 * sizeof(int) * (8192 + 1)));
+    if (e != hipSuccess) return e;
     attr_set = true;
   }
   hipLaunchKernelGGL(sp_sort_kernel, dim3(g.sp_nchunk), dim3(kT), lds_sort, s, g.N, g.Kp,
@@ -564,9 +577,9 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   hipLaunchKernelGGL(sp_rowscan_kernel, dim3((g.Kp + kT / 64 - 1) / (kT / 64)), dim3(kT), 0, s,
                      g.Kp, g.sp_nchunk, sp.cnt, sp.rowtot);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_top_kernel, dim3(1), dim3(kScanThreads), sizeof(int) * (g.Kp + 1), s,
+  hipLaunchKernelGGL(sp_top_kernel, dim3(1), dim3(kScanThreads), 2 * sizeof(int) * (g.Kp + 1), s,
                      g.N, g.Kp, g.sp_nchunk,
-                     sp_piece_budget(g), sp.rowtot, sp.ocnt, sp.xsum, sp.seg, sp.pstart, sp.pcomp, sp.nov, sp.glob,
+                     sp_piece_budget(g), sp.rowtot, sp.ocnt, sp.xsum, sp.seg, sp.pstart, sp.pinfo, sp.nov, sp.glob,
                      sp.kmap, sp.nflag);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(sp_place_kernel, dim3(g.sp_nchunk), dim3(kT), sizeof(int) * (size_t)g.Kp,
@@ -581,7 +594,7 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   const long cap = sp_npiece_cap(g);
   const long gg = cap / 8 < kGroupGrid ? kGroupGrid : (cap / 8 > kPieceGrid ? kPieceGrid : cap / 8);
   hipLaunchKernelGGL(sp_group_kernel, dim3(cap < gg ? cap : gg), dim3(kT), 0, s, g.d, g.dp,
-                     g.stat_w, sp.pstart, sp.pcomp, sp.nov, sp.prow);
+                     g.stat_w, sp.pinfo, sp.nov, sp.prow);
   return hipGetLastError();
 }
 
