@@ -49,6 +49,7 @@ constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
 constexpr int kAccUnroll = 4;      // entries per lane group in flight
+constexpr int kPre = 4;            // list entries per point requested ahead in the chunk sort
 constexpr int kSpCountMax = 2048;  // up to this Kp the chunk sort is a counting sort
 constexpr int kPieceGrid = 2048;   // workgroups of the piece kernel (grid-stride)
 constexpr int kGroupGrid = 256;    // group fold: at least this many workgroups (grid-stride),
@@ -106,15 +107,24 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     ek_sh = 0;
     ep_sh = 0;
   }
-  // one point per thread
+  // one point per thread; its log-normalizer and first kPre entries are
+  // requested before the scan (i < m <= C: in bounds)
   const long n = p0 + tid;
   int m = 0, ov = 0;
-  double s1 = 0.0;
+  double s1 = 0.0, l2 = 0.0;
+  int kpre[kPre];
+  double vpre[kPre];
   if (n < N) {
     const int c = pcnt[n];
     s1 = (double)xm[n];
+    l2 = ln2[n];
     if (c > C) ov = 1;
     else m = c;
+#pragma unroll
+    for (int i = 0; i < kPre; i++) {
+      kpre[i] = i < m ? pk[(size_t)n * C + i] : 0;
+      vpre[i] = i < m ? pv[(size_t)n * C + i] : 0.0;
+    }
   }
   const int pos = block_excl_scan<kT>(m, sh, nullptr);
   // entries of the kept points -> LDS keys (component, point) and gamma.
@@ -126,13 +136,11 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     atomicMin(&cut_sh, tid);
     ov = 1;
   } else if (m > 0) {
-    const double l2 = ln2[n];
     const int* kr = pk + (size_t)n * C;
     const double* vr = pv + (size_t)n * C;
-    for (int i = 0; i < m; i++) {
-      const int kb = kr[i];
+    auto put = [&](int i, int kb, double v) {
       const int k = kb & (kSpBound - 1);
-      float gam = exp2f((float)(vr[i] - l2));
+      float gam = exp2f((float)(v - l2));
       if (kb & kSpBound) gam *= 1.0f + 0x1p-20f;   // stays an upper bound
       // below 2^-126 the pair joins the per-(point, component) floor
       const bool keep = gam >= 0x1p-126f;
@@ -142,7 +150,11 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
         atomicAdd(&hist[k], 1);   // integer counts: order-free
         mine++;
       }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < kPre; i++)
+      if (i < m) put(i, kpre[i], vpre[i]);
+    for (int i = kPre; i < m; i++) put(i, kr[i], vr[i]);
     atomicMax(&ep_sh, pos + m);
   }
   atomicAdd(&ov_sh, ov);
