@@ -1,23 +1,46 @@
 """Benchmark: fused Flash-GMM EM iterations per second on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--config 2] [--all]
-                    [--variant auto|valu|mfma|x32|mixed|sparse] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--config 2]
+                    [--configs 1,2,3,4,5] [--variant auto|valu|mfma|x32|mixed|sparse]
+                    [--no-cpu-baseline] [--cpu-seconds S]
 
 A step is one fused EM iteration (precompute -> Pass 1 -> Pass 2 ->
 reduction/M-step) over the configuration's full synthetic data set, which is
 resident in HBM before timing starts.  The timed region runs ``steps``
 iterations back to back on the device (parameters fed forward on the device,
 no host synchronisation inside), bracketed by ``torch.cuda.synchronize()``.
-Each pass's launch durations are measured live with HIP events on the launch
-stream (``fgmm_profile_*``); the dominant kernel's give the roofline figure.
 
-Default workload: configuration 2 (N=65536, K=256, d=128, fp32), the metric's
-headline shape.  ``--all`` adds one JSON line per configuration after the
-headline line.  The CPU baseline is the reference's own C++/OpenMP standard
-E+M (``flash_gmm_cpu.cpp`` standard_e_step + standard_m_step) compiled into
-``oracle/_ref``, timed on a bounded sample of the same workload on rank 0;
-if that build is absent, this repository's fp32 restatement of it
-(``oracle/fgmm_oracle.c``) is timed instead and labelled "port".
+Each configuration runs twice after the warm-up:
+  * a clean run: its wall time is ``value`` / ``ms_per_step``;
+  * a profiled run: HIP events on the launch stream around every pass
+    (``fgmm_profile_*``) give the per-pass durations and the dominant
+    kernel's roofline; its own wall time is reported beside the event sums,
+    which it contains.
+
+ONE JSON line is printed.  Its top level describes the headline
+configuration (default C2: N=65536, K=256, d=128, fp32, the metric's shape);
+``configs`` holds the same figures for every configuration in --configs
+(default all five; C5 runs its own 10-iteration step count).
+
+Roofline figures are utilisation of the units that execute the work:
+  * ``roofline``: the dominant kernel's issued work against its unit's peak.
+    For the sparse variant's Pass 1 that is the bf16 matrix-core sweep,
+    3 x 4NKd products (operands split hi + lo), against 2.5 PFLOP/s.
+  * ``work_model``: the iteration's executed work -- the issued matrix-core
+    flops at their precisions, the fp64 work on the listed pairs, the
+    algorithmic HBM bytes -- priced at the peaks, over the measured time.
+The metric's own framing (4NKd fp32-class products per Pass 1 against the
+157.3 TFLOP/s fp32 matrix-core peak) is kept as a rate,
+``fp32_class_tflops``, and as ``t_fp32_roofline_over_t`` (how many times
+faster than an fp32 matrix-core kernel at peak could run the same products):
+a ratio, not a utilisation.
+
+The CPU baseline is the reference's own C++/OpenMP standard E+M
+(``flash_gmm_cpu.cpp`` standard_e_step + standard_m_step) compiled into
+``oracle/_ref``, timed on all host cores on a bounded sample of each
+configuration on rank 0; if that build is absent, this repository's fp32
+restatement of it (``oracle/fgmm_oracle.c``) is timed instead and labelled
+"port".
 """
 from __future__ import annotations
 
@@ -39,6 +62,7 @@ HBM_PEAK = 8.0e12        # B/s, MI355X
 FP32_PEAK = 157.3e12     # FLOP/s, MI355X dense fp32 (vector = matrix)
 FP64_PEAK = 78.6e12      # FLOP/s, MI355X dense fp64 (vector = matrix)
 BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 matrix cores
+METRIC = "EM iters/s (N=65536,K=256,d=128 fp32) + % of HBM / fp32-MFMA roofline"
 
 
 def parse():
@@ -47,11 +71,12 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
-    ap.add_argument("--all", action="store_true", help="also report every configuration")
+    ap.add_argument("--configs", default=",".join(str(c) for c in sorted(CONFIGS)),
+                    help="configurations reported in the line's `configs` array")
     ap.add_argument("--variant", default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0,
-                    help="target CPU time for the baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=4.0,
+                    help="target CPU time per configuration for the baseline sample")
     ap.add_argument("--stream-chunk", type=int, default=0,
                     help="instead of the resident benchmark, time the streaming iteration "
                          "(X in pinned host memory, chunks of this many rows copied while "
@@ -73,20 +98,9 @@ def copy_probe(mib: int) -> None:
     del src, dst
 
 
-def pass2_peak() -> float:
-    # Pass 2's 8 flops per (n,k,j) run at different precisions: the distance
-    # recompute (4) and sum gamma*x^2 (2) on fp64 matrix cores, sum gamma*x (2)
-    # on fp32 matrix cores.  The binding peak is the time-weighted mix.
-    return 8.0 / (6.0 / FP64_PEAK + 2.0 / FP32_PEAK)
-
-
-FP32_SWEEP = ("x32", "mixed")   # Pass 1 on fp32 matrix cores
-BF16_SWEEP = ("sparse",)        # Pass 1 on bf16 matrix cores, operands split hi + lo
-
-
 def arithmetic_type(variant: str) -> str:
     """What the variant computes in (inputs and outputs are fp32 throughout)."""
-    if variant in BF16_SWEEP:
+    if variant == "sparse":
         return ("f64 (pairs near each point's maximum, statistics, reduction) + "
                 "bf16x3 matrix-core bound sweep with fp32 accumulation")
     if variant == "x32":
@@ -97,48 +111,124 @@ def arithmetic_type(variant: str) -> str:
     return "f64 (vector ALU)"
 
 
-def dominant_roofline(cfg, variant, kernels):
-    """Roofline of the kernel that takes the most time per iteration.
+def padded(cfg, variant):
+    """(Kp, dp, dpb) as the library pads them for the matrix-core kernels."""
+    Kp = (cfg.K + 31) // 32 * 32
+    dp = (cfg.d + 15) // 16 * 16
+    return Kp, dp, (dp + 31) // 32 * 32
 
-    Pass 1 is a dense sweep over all (n, k): 4 flops per (n, k, j) (the
-    x^2 and x contractions), on fp32 matrix cores for x32 and mixed, on fp64
-    matrix cores (fp64 VALU for valu) for mfma/valu, and for sparse on bf16
-    matrix cores with each operand split into bf16 hi + lo, three products
-    (lo*hi, hi*lo, hi*hi) per algorithmic product.  The metric prices the
-    algorithmic 4NKd against the fp32 matrix-core peak; for the bf16 sweep
-    the issued matrix-core work (3 x 4NKd) against the bf16 peak is reported
-    beside it.  The dense Pass 2 recomputes the distance and accumulates
-    gamma^T [X, X^2]: 8 flops per (n, k, j) at its fp64/fp32 instruction mix.
-    The sparse variant's Pass 2 touches only the listed pairs and is not
-    dominant."""
+
+def pass_work(cfg, variant, which):
+    """(issued flops per launch, peak FLOP/s of that instruction mix, unit)
+    of Pass 1 or Pass 2 over the padded problem (Kp, dp / dpb).
+
+    Pass 1: sparse issues 3 bf16 products (lo*hi, hi*lo, hi*hi of the split
+    operands) per fp32-class product, 2 flops each, over the Kp x 2dpb
+    contraction; x32 / mixed one fp32 product over Kp x 2dp; mfma one fp64
+    product.  Pass 2 (dense): the distance recompute (Kp x 2dp) plus
+    sum gamma x (dp) and sum gamma x^2 (dp) per pair -- mfma / mixed: the
+    distance and sum gamma x^2 on fp64, sum gamma x on fp32 matrix cores;
+    x32: distance and sum gamma x on fp32, sum gamma x^2 on fp64.  The peak of
+    a mix is its time-weighted one.  valu: 4NKd (Pass 1) or 8NKd (Pass 2) on
+    the fp64 vector ALU."""
+    N = float(cfg.N)
+    Kp, dp, dpb = padded(cfg, variant)
+    if variant == "valu":
+        f = (4.0 if which == 1 else 8.0) * N * cfg.K * cfg.d
+        return f, FP64_PEAK, "fp64 vector ALU"
+    if which == 1:
+        if variant == "sparse":
+            return 3 * 2 * N * Kp * 2 * dpb, BF16_PEAK, "bf16 matrix cores"
+        if variant in ("x32", "mixed"):
+            return 2 * N * Kp * 2 * dp, FP32_PEAK, "fp32 matrix cores"
+        return 2 * N * Kp * 2 * dp, FP64_PEAK, "fp64 matrix cores"
+    dist, half = 2 * N * Kp * 2 * dp, 2 * N * Kp * dp
+    if variant == "x32":
+        f32, f64 = dist + half, half
+    else:
+        f32, f64 = half, dist + half
+    return f32 + f64, (f32 + f64) / (f32 / FP32_PEAK + f64 / FP64_PEAK), "fp64/fp32 matrix cores"
+
+
+def dominant_roofline(cfg, variant, kernels):
+    """Utilisation of the kernel that takes the most time per iteration: its
+    issued work per launch (pass_work) over its average launch duration,
+    against the peak of the units that execute it.  The sparse variant's
+    Pass 2 works on the listed pairs only and is never the dense sweep, so
+    Pass 1 is its kernel."""
     nkd = float(cfg.N) * cfg.K * cfg.d
     t1 = kernels["pass1"]["ms_avg"] / 1e3
     t2 = kernels["pass2"]["ms_avg"] / 1e3
-    if variant == "sparse" or t1 >= t2:
-        if variant in BF16_SWEEP:
-            peak, unit = FP32_PEAK, "bf16 matrix cores, split operands"
-        elif variant in FP32_SWEEP:
-            peak, unit = FP32_PEAK, "fp32 matrix cores"
-        else:
-            peak, unit = FP64_PEAK, "fp64"
-        flops, t = 4.0 * nkd, t1
-        out = {"kernel": f"pass1 (log-normalizer sweep, {unit})", "peak": peak / 1e12}
-        if variant in BF16_SWEEP and t > 0:
-            issued = 3.0 * flops
-            out["issued_bf16_mfma"] = {"flops_per_launch": issued,
-                                       "achieved": issued / t / 1e12, "peak": BF16_PEAK / 1e12,
-                                       "unit": "TFLOP/s", "frac": issued / t / BF16_PEAK}
+    which = 1 if (variant == "sparse" or t1 >= t2) else 2
+    t = t1 if which == 1 else t2
+    issued, peak, unit = pass_work(cfg, variant, which)
+    name = ("pass1 (log-normalizer sweep" if which == 1
+            else "pass2 (gamma recompute + sufficient statistics")
+    achieved = issued / t if t > 0 else 0.0
+    out = {"kernel": f"{name}, {unit})", "bound": "mfma", "achieved": achieved / 1e12,
+           "peak": peak / 1e12, "unit": "TFLOP/s", "frac": achieved / peak,
+           "flops_per_launch": issued, "launch_ms": t * 1e3}
+    if which == 1 and variant in ("sparse", "x32", "mixed") and t > 0:
+        out["fp32_class_tflops"] = 4 * nkd / t / 1e12
+        out["t_fp32_roofline_over_t"] = (4 * nkd / FP32_PEAK) / t
+    return out
+
+
+def work_model(cfg, variant, ms_per_step, counts):
+    """Executed work of one iteration priced at the units' peaks.
+
+    sparse: the bf16 sweep (3 x 2 x N x Kp x 2dpb), fp64 work on the listed
+    entries (Pass 1 evaluates each exactly: ~4 flops per feature; Pass 2
+    accumulates gamma, gamma x, gamma x^2: 4 flops per feature), the dense
+    fp64 pass over the components the reduction flagged (8 x N x 16 x dp
+    per 16-component subtile), and HBM bytes: X read by both passes, the
+    lists written and read (12 B per entry), the log-normalizer and
+    parameters.  Dense variants: both passes' issued work (pass_work)."""
+    N = float(cfg.N)
+    Kp, dp, dpb = padded(cfg, variant)
+    B = cfg.bytes_per_iter()
+    if variant == "sparse":
+        E = float(counts.get("entries", 0))
+        flagged = float(counts.get("flagged", 0))
+        t_mfma = 3 * 2 * N * Kp * 2 * dpb / BF16_PEAK
+        f64 = E * 4 * cfg.d * 2 + ((flagged + 15) // 16) * 16 * 8 * N * dp
+        t_f64 = f64 / FP64_PEAK
+        B += 2 * 12 * E
+        parts = {"bf16_sweep_us": t_mfma * 1e6, "fp64_us": t_f64 * 1e6,
+                 "listed_entries": int(E), "flagged_components": int(flagged)}
+        t_c = t_mfma + t_f64
     else:
-        flops, t = 8.0 * nkd, t2
-        peak = FP32_PEAK
-        out = {"kernel": "pass2 (gamma recompute + sufficient statistics)",
-               "peak": peak / 1e12,
-               "peak_at_kernel_precision": pass2_peak() / 1e12}
-    achieved = flops / t if t > 0 else 0.0
-    out.update({"bound": "mfma", "achieved": achieved / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / peak, "flops_per_launch": flops})
-    if "peak_at_kernel_precision" in out:
-        out["frac_at_kernel_precision"] = achieved / pass2_peak()
+        f1, p1, _ = pass_work(cfg, variant, 1)
+        f2, p2, _ = pass_work(cfg, variant, 2)
+        t_c = f1 / p1 + f2 / p2
+        parts = {"pass1_us": f1 / p1 * 1e6, "pass2_us": f2 / p2 * 1e6}
+    t_b = B / HBM_PEAK
+    t_model = max(t_c, t_b)
+    t = ms_per_step / 1e3
+    return {"t_model_us": t_model * 1e6, "bound": "compute" if t_c >= t_b else "hbm",
+            "compute_us": t_c * 1e6, "hbm_us": t_b * 1e6, "hbm_bytes": B,
+            "frac": t_model / t if t > 0 else 0.0, **parts}
+
+
+def sparse_counts(lib, cfg, variant, ws):
+    """Counts of the last timed iteration, read from the workspace."""
+    import torch
+    if variant != "sparse":
+        return {}
+    out = {}
+    vcode = 5
+    for name in ("pcnt", "nflag"):
+        off, nb = ctypes.c_size_t(), ctypes.c_size_t()
+        if lib.fgmm_workspace_region(cfg.N, cfg.K, cfg.d, vcode, name.encode(),
+                                     ctypes.byref(off), ctypes.byref(nb)) != 0:
+            return {}
+        view = ws[off.value:off.value + nb.value].view(torch.int32)
+        if name == "pcnt":
+            cap = min(cfg.K, 32)
+            out["entries"] = int(view.clamp(max=cap).sum().item())
+            out["overflow_points"] = int((view > cap).sum().item())
+        else:
+            out["flagged"] = int(view[0].item())
     return out
 
 
@@ -156,34 +246,37 @@ def run_gpu(cid, steps, warmup, variant):
     lp = torch.from_numpy(lp0).to(dev)
     lib = _lib.load()
     vname = C.resolve_variant(cfg.N, cfg.K, cfg.d, variant)
+    wsb = lib.fgmm_workspace_bytes(cfg.N, cfg.K, cfg.d, _lib.variant_code(variant))
 
-    # warmup (also builds the workspace)
-    if warmup > 0:
+    if warmup > 0:   # also builds the workspace
         C.em_fit(Xd, mu, var, lp, warmup, variant=variant)
     torch.cuda.synchronize()
+    # clean run: the headline
+    t0 = time.perf_counter()
+    _, _, _, traj = C.em_fit(Xd, mu, var, lp, steps, variant=variant)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    counts = sparse_counts(lib, cfg, vname, _lib.workspace(dev, wsb))
+    # profiled run: per-pass HIP events on the launch stream
     _lib.check(lib.fgmm_profile_enable(1))
     ms = (ctypes.c_double * 4)()
     cnt = (ctypes.c_long * 4)()
     _lib.check(lib.fgmm_profile_read(ms, cnt))  # reset
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    mu_o, var_o, lp_o, traj = C.em_fit(Xd, mu, var, lp, steps, variant=variant)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    _lib.check(lib.fgmm_profile_read(ms, cnt))
-    _lib.check(lib.fgmm_profile_enable(0))
-    # the same loop without events, for the headline number
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     C.em_fit(Xd, mu, var, lp, steps, variant=variant)
     torch.cuda.synchronize()
-    elapsed_clean = time.perf_counter() - t0
+    elapsed_prof = time.perf_counter() - t0
+    _lib.check(lib.fgmm_profile_read(ms, cnt))
+    _lib.check(lib.fgmm_profile_enable(0))
     ll = traj.cpu().numpy()
-    kern = {name: {"ms_avg": ms[i] / max(cnt[i], 1), "launches": int(cnt[i])}
+    kern = {name: {"ms_avg": ms[i] / max(cnt[i], 1), "launches": int(cnt[i]),
+                   "ms_per_step": ms[i] / steps}
             for i, name in enumerate(["precompute", "pass1", "pass2", "reduce_mstep"])}
-    return {"elapsed": min(elapsed, elapsed_clean), "elapsed_profiled": elapsed,
-            "kernels": kern, "ll_first": float(ll[0]), "ll_last": float(ll[-1]),
-            "variant": vname}
+    del Xd, mu, var, lp
+    return {"elapsed": elapsed, "elapsed_profiled": elapsed_prof, "kernels": kern,
+            "ll_first": float(ll[0]), "ll_last": float(ll[-1]), "variant": vname,
+            "workspace_bytes": int(wsb), "counts": counts}
 
 
 def run_stream(cid, steps, warmup, chunk, variant):
@@ -224,7 +317,9 @@ def run_stream(cid, steps, warmup, chunk, variant):
 
 
 def cpu_baseline(cid, budget_s):
-    """Times the reference's standard E+M on the host (bounded sample)."""
+    """Times the reference's standard E+M on the host (bounded sample: one
+    warm-up iteration, then iterations until the budget is spent, at least
+    one, at most the configuration's iteration count)."""
     import torch
     from oracle import oracle as O
 
@@ -275,39 +370,39 @@ def measured_traffic(cid, variant, kernel):
     return None if r is None else r["read_bytes"] + r["write_bytes"]
 
 
-def line_for(cid, args, with_cpu):
+def measure(cid, args, with_cpu):
     cfg = CONFIGS[cid]
-    r = run_gpu(cid, args.steps, args.warmup, args.variant)
+    steps = cfg.iters if cid == 5 else args.steps
+    print(f"[bench] C{cid}: N={cfg.N} K={cfg.K} d={cfg.d}, {steps} steps", file=sys.stderr,
+          flush=True)
+    r = run_gpu(cid, steps, args.warmup, args.variant)
     sec = r["elapsed"]
-    its = args.steps / sec
-    F_total = cfg.flops_per_iter()
-    roof_t = max(F_total / FP32_PEAK, cfg.bytes_per_iter() / HBM_PEAK)
+    ms_step = sec * 1e3 / steps
     roof = dominant_roofline(cfg, r["variant"], r["kernels"])
     roof["traffic"] = measured_traffic(cid, r["variant"], roof["kernel"])
-    roof["traffic_unit"] = "HBM bytes/launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE, profiles/)"
+    roof["traffic_unit"] = ("HBM bytes/launch (rocprofv3 FETCH_SIZE and WRITE_SIZE, scaled "
+                            "by a plain copy's reading; profiles/)")
+    ev_sum = sum(k["ms_per_step"] for k in r["kernels"].values())
     out = {
-        "metric": "EM iters/s (N=65536,K=256,d=128 fp32) + % of HBM / fp32-MFMA roofline",
-        "value": its,
-        "unit": "EM iters/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": sec * 1e3 / args.steps,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": arithmetic_type(r["variant"]),
-        "data": "synthetic (seeded mixture generator, flashgmm_amd/configs.py)",
-        "config": {"workload": f"C{cid}: diag-cov GMM EM N={cfg.N} K={cfg.K} d={cfg.d} fp32",
-                   "N": cfg.N, "K": cfg.K, "d": cfg.d, "kernel_variant": r["variant"]},
+        "config": cid, "N": cfg.N, "K": cfg.K, "d": cfg.d, "variant": r["variant"],
+        "steps": steps, "value": steps / sec, "ms_per_step": ms_step,
         "roofline": roof,
-        "iteration_roofline_frac": roof_t / (sec / args.steps),
-        "kernels_ms": {k: v["ms_avg"] for k, v in r["kernels"].items()},
-        "ll_first": r["ll_first"],
-        "ll_last": r["ll_last"],
+        "work_model": work_model(cfg, r["variant"], ms_step, r["counts"]),
+        "timing": {
+            "profiled_run_ms_per_step": r["elapsed_profiled"] * 1e3 / steps,
+            "event_sum_ms_per_step": ev_sum,
+            "kernels_ms_per_launch": {k: v["ms_avg"] for k, v in r["kernels"].items()},
+            "note": "events are recorded in the profiled run only; their sum per step is "
+                    "part of that run's wall time (the rest is host queueing and the gaps "
+                    "between launches); value comes from the clean run",
+        },
+        "workspace_bytes": r["workspace_bytes"],
+        "x_bytes": cfg.N * cfg.d * 4,
+        "ll_first": r["ll_first"], "ll_last": r["ll_last"],
     }
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline(cid, args.cpu_seconds)
+        out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     return out
 
 
@@ -325,16 +420,39 @@ def main():
             print(json.dumps(run_stream(args.config, args.steps, args.warmup, args.stream_chunk,
                                         args.variant)), flush=True)
         return
-    head = line_for(args.config, args, with_cpu=(rank == 0 and not args.no_cpu_baseline))
+    with_cpu = rank == 0 and not args.no_cpu_baseline
+    cids = [int(c) for c in args.configs.split(",") if c.strip()]
+    if args.config not in cids:
+        cids.insert(0, args.config)
+    per = {cid: measure(cid, args, with_cpu) for cid in cids}
+    h = per[args.config]
+    cfg = CONFIGS[args.config]
+    line = {
+        "metric": METRIC,
+        "value": h["value"],
+        "unit": "EM iters/s",
+        "n_gpus": 1,
+        "steps": h["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": arithmetic_type(h["variant"]),
+        "data": "synthetic (seeded mixture generator, flashgmm_amd/configs.py)",
+        "config": {"workload": f"C{args.config}: diag-cov GMM EM N={cfg.N} K={cfg.K} "
+                               f"d={cfg.d} fp32",
+                   "N": cfg.N, "K": cfg.K, "d": cfg.d, "kernel_variant": h["variant"]},
+        "roofline": h["roofline"],
+        "work_model": h["work_model"],
+        "timing": h["timing"],
+        "workspace_bytes": h["workspace_bytes"],
+    }
+    if "cpu_baseline" in h:
+        line["cpu_baseline"] = h["cpu_baseline"]
+    line["configs"] = [per[c] for c in sorted(per)]
     if rank == 0:
-        print(json.dumps(head), flush=True)
-    if args.all:
-        for cid in sorted(CONFIGS):
-            if cid == args.config:
-                continue
-            o = line_for(cid, args, with_cpu=False)
-            if rank == 0:
-                print(json.dumps(o), flush=True)
+        print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

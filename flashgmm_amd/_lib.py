@@ -25,6 +25,10 @@ SIGNATURES = {
     "fgmm_version": ([], _I),
     "fgmm_last_error": ([], ctypes.c_char_p),
     "fgmm_resolve_variant": ([_L, _I, _I, _I], _I),
+    "fgmm_error_model": ([_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
+                         _I),
+    "fgmm_workspace_region": ([_L, _I, _I, _I, ctypes.c_char_p, ctypes.POINTER(_Z),
+                               ctypes.POINTER(_Z)], _I),
     "fgmm_workspace_bytes": ([_L, _I, _I, _I], _Z),
     "fgmm_em_fused": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _P, _P, _Z, _P], _I),
     "fgmm_log_normalizer": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _Z, _P], _I),

@@ -464,6 +464,42 @@ int fgmm_resolve_variant(long N, int K, int d, int variant) {
   return resolve_variant(N, K, d, variant);
 }
 
+int fgmm_error_model(int d, double* c_x32, double* c_bf16) {
+  g_err[0] = 0;
+  if (d < 1 || d > kMaxD) return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
+  FGMM_REQUIRE(c_x32);
+  FGMM_REQUIRE(c_bf16);
+  const int dp = round_up(d, 16);
+  *c_x32 = x32_err_c(dp);
+  *c_bf16 = x32_err_c_bf(sp_dpb(dp));
+  return FGMM_OK;
+}
+
+int fgmm_workspace_region(long N, int K, int d, int variant, const char* name,
+                          size_t* offset, size_t* bytes) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(name); FGMM_REQUIRE(offset); FGMM_REQUIRE(bytes);
+  Geom g = make_geom(N, K, d, variant);
+  if (g.variant != kSparse)
+    return fail(FGMM_EINVAL, "workspace regions are published for the sparse variant only");
+  WsLayout L = make_layout(g);
+  // carve views relative to a stand-in base (never dereferenced)
+  char* base = reinterpret_cast<char*>(uintptr_t(1) << 40);
+  Ws w = carve(g, base, L);
+  const char* p = nullptr;
+  size_t n = 0;
+  if (!strcmp(name, "pcnt")) { p = reinterpret_cast<char*>(w.x.pcnt); n = sizeof(int) * (size_t)N; }
+  else if (!strcmp(name, "rowtot")) { p = reinterpret_cast<char*>(w.sp.rowtot); n = sizeof(int) * (size_t)g.Kp; }
+  else if (!strcmp(name, "nov")) { p = reinterpret_cast<char*>(w.sp.nov); n = sizeof(int) * 3; }
+  else if (!strcmp(name, "nflag")) { p = reinterpret_cast<char*>(w.sp.nflag); n = sizeof(int); }
+  else return fail(FGMM_EINVAL, "unknown workspace region '%s'", name);
+  *offset = (size_t)(p - base);
+  *bytes = n;
+  return FGMM_OK;
+}
+
 size_t fgmm_workspace_bytes(long N, int K, int d, int variant) {
   if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
   return make_layout(make_geom(N, K, d, variant)).total;

@@ -234,12 +234,14 @@ def m_step_update(n_k, s_k, sq_k, N: int):
     if N < 1:
         raise RuntimeError("flashgmm_amd.m_step_update: N must be >= 1")
     lib = _lib.load()
+    # the contiguous copies stay bound until the call has been queued: a
+    # temporary freed earlier could hand its block to the next copy
+    n_c, s_c, sq_c = n_k.contiguous(), s_k.contiguous(), sq_k.contiguous()
     mu = torch.empty((K, d), dtype=torch.float32, device=s_k.device)
     var = torch.empty((K, d), dtype=torch.float32, device=s_k.device)
     log_pi = torch.empty((K,), dtype=torch.float32, device=s_k.device)
-    _lib.check(lib.fgmm_m_step_update(_ptr(n_k.contiguous()), _ptr(s_k.contiguous()),
-                                      _ptr(sq_k.contiguous()), N, K, d, _ptr(mu), _ptr(var),
-                                      _ptr(log_pi), _lib.stream_handle(s_k.device)))
+    _lib.check(lib.fgmm_m_step_update(_ptr(n_c), _ptr(s_c), _ptr(sq_c), N, K, d, _ptr(mu),
+                                      _ptr(var), _ptr(log_pi), _lib.stream_handle(s_k.device)))
     return [mu, var, log_pi]
 
 

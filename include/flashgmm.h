@@ -61,6 +61,30 @@ const char* fgmm_last_error(void);
 /* Variant the library will run for (K, d) when asked for `variant`. */
 int fgmm_resolve_variant(long N, int K, int d, int variant);
 
+/*
+ * Constants of the rigorous error bounds of the fp32-class distance sweeps
+ * (host-only query, no device work): with a0 = sum_j P1_kj x_j^2 (the x^2
+ * half of the expanded distance, P1 = -log2(e)/(2 var)), bias_k the expanded
+ * bias and D_k = log2(e)/2 sum_j mu_kj^2/var_kj, a sweep's log2-density
+ * differs from the exact one by at most c (|bias_k| + D_k + 2 |a0|):
+ * c_x32 for the fp32 matrix-core sweep (x32, mixed), c_bf16 for the bf16
+ * hi/lo split sweep (sparse).  No counterpart in the reference (its fp32
+ * kernels carry no error bound).
+ */
+int fgmm_error_model(int d, double* c_x32, double* c_bf16);
+
+/*
+ * Diagnostic view of the sparse variant's workspace (host-only query): byte
+ * offset and size of a named region that holds, after a call, counts of the
+ * last iteration -- "pcnt" (int [N]: list entries of each point, more than
+ * min(K, 32) = the point took the dense path), "rowtot" (int [Kp]: listed
+ * entries per component), "nov" (int [3]: overflow points, accumulation
+ * pieces, entries per piece), "nflag" (int: components recomputed exactly).
+ * FGMM_EINVAL for other variants or names.  No counterpart in the reference.
+ */
+int fgmm_workspace_region(long N, int K, int d, int variant, const char* name,
+                          size_t* offset, size_t* bytes);
+
 /* Workspace bytes needed by every entry point below for this problem. */
 size_t fgmm_workspace_bytes(long N, int K, int d, int variant);
 

@@ -302,17 +302,32 @@ def c32_em_fused(X, mu, var, log_pi, BK=8):
     return nm, nv, nl, ln
 
 
-def c32_standard_em(X, mu, var, log_pi):
-    """Reference-order fp32 standard E-step + M-step
-    (flash_gmm_cpu.cpp:51-100 then :292-311)."""
+def c32_standard_e_step(X, mu, var, log_pi):
+    """Reference-order fp32 standard E-step (flash_gmm_cpu.cpp:51-100);
+    returns (gamma [N, K], log_normalizer [N])."""
     X, mu, var, log_pi = map(_f32, (X, mu, var, log_pi))
     N, d = X.shape
     K = mu.shape[0]
     g, ln = np.empty((N, K), np.float32), np.empty(N, np.float32)
     clib().orc32_standard_e_step(X, mu, var, log_pi, N, K, d, g, ln)
+    return g, ln
+
+
+def c32_standard_m_step(X, gamma):
+    """fp32 standard M-step (flash_gmm_cpu.cpp:292-311); returns (mu, var, log_pi)."""
+    X, gamma = _f32(X), _f32(gamma)
+    N, d = X.shape
+    K = gamma.shape[1]
     m, v, lp = np.empty((K, d), np.float32), np.empty((K, d), np.float32), np.empty(K, np.float32)
-    clib().orc32_standard_m_step(X, g, N, K, d, m, v, lp)
-    return m, v, lp, ln
+    clib().orc32_standard_m_step(X, gamma, N, K, d, m, v, lp)
+    return m, v, lp
+
+
+def c32_standard_em(X, mu, var, log_pi):
+    """Reference-order fp32 standard E-step + M-step
+    (flash_gmm_cpu.cpp:51-100 then :292-311)."""
+    g, ln = c32_standard_e_step(X, mu, var, log_pi)
+    return (*c32_standard_m_step(X, g), ln)
 
 
 def c_num_threads():

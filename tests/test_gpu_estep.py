@@ -4,7 +4,8 @@ and the standard M-step, through the C ABI, against the fp64 oracle.
 Tolerances:
   * gamma: absolute error <= 1e-6 (gamma lies in [0, 1]);
   * log_normalizer: relative error <= 1e-5;
-  * standard M-step mu, var: |gpu - fp64| <= max(1e-5, 2 ulp_fp32(value)),
+  * standard M-step mu, var: |gpu - fp64| <= 1e-5 below 256, one fp32 ulp from 256 up
+    (parity_util.param_tol),
     pi = exp(log_pi): <= 1e-5 -- from the same fp32 gamma the device gets;
   * NativeStandardGMM mean log-likelihood trajectory: relative <= 1e-4.
 """

@@ -1,7 +1,7 @@
 """Streaming EM iteration (X fed in chunks from host or device memory)
 against the fp64 oracle and against the resident fused iteration.
 
-Tolerances: mu, var |gpu - fp64| <= max(1e-5, 2 ulp_fp32); pi <= 1e-5; the
+Tolerances: mu, var |gpu - fp64| <= 1e-5 (one fp32 ulp from 256 up); pi <= 1e-5; the
 log-normalizer is per point, so it must equal the resident Pass 1 bit for
 bit; the mean log-likelihood matches the oracle to 1e-10 relative.
 """
