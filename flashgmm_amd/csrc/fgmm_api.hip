@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "../../include/flashgmm.h"
@@ -450,6 +451,55 @@ static int stream_variant(int K, int d, int variant) {
   return variant == kX32 ? kMfma : variant;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch of the allocation-free entry point.  One copy per GPU the
+// library runs on, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in); it uses the
+// device address hipGetSymbolAddress returns, kept per device.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices] = {};
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch (resolved once per device).
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FGMM_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FGMM_EINVAL, "device ordinal %d out of range for the static scratch", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(FGMM_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FGMM_OK;
+}
+
+static int em_fused_impl(const float* X, const float* mu, const float* var,
+                         const float* log_pi, long N, int K, int d, int variant, float* new_mu,
+                         float* new_var, float* new_log_pi, float* log_normalizer, void* ws,
+                         size_t ws_bytes, void* stream) {
+  Geom g = make_geom(N, K, d, variant);
+  WsLayout L = make_layout(g);
+  int rc = validate_ws(g, L, ws, ws_bytes);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Ws w = carve(g, ws, L);
+  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
+  if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
+  if ((rc = run_pass2(g, X, w, s))) return rc;
+  return run_reduce(g, X, w, new_mu, new_var, new_log_pi, nullptr, nullptr, nullptr, s);
+}
+
 }  // namespace fgmm
 
 using namespace fgmm;
@@ -515,15 +565,32 @@ int fgmm_em_fused(const float* X, const float* mu, const float* var, const float
   FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
   FGMM_REQUIRE(new_mu); FGMM_REQUIRE(new_var); FGMM_REQUIRE(new_log_pi);
   FGMM_REQUIRE(log_normalizer);
-  Geom g = make_geom(N, K, d, variant);
-  WsLayout L = make_layout(g);
-  if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  Ws w = carve(g, ws, L);
-  if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
-  if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
-  if ((rc = run_pass2(g, X, w, s))) return rc;
-  return run_reduce(g, X, w, new_mu, new_var, new_log_pi, nullptr, nullptr, nullptr, s);
+  return em_fused_impl(X, mu, var, log_pi, N, K, d, variant, new_mu, new_var, new_log_pi,
+                       log_normalizer, ws, ws_bytes, stream);
+}
+
+size_t fgmm_em_fused_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int fgmm_em_fused_noalloc(const float* X, const float* mu, const float* var,
+                          const float* log_pi, long N, int K, int d, int variant, float* new_mu,
+                          float* new_var, float* new_log_pi, float* log_normalizer,
+                          void* stream) {
+  g_err[0] = 0;
+  int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
+  FGMM_REQUIRE(new_mu); FGMM_REQUIRE(new_var); FGMM_REQUIRE(new_log_pi);
+  FGMM_REQUIRE(log_normalizer);
+  const size_t need = make_layout(make_geom(N, K, d, variant)).total;
+  if (need > kScratchBytes)
+    return fail(FGMM_EWORKSPACE,
+                "problem N=%ld K=%d d=%d needs %zu bytes of scratch; the allocation-free entry "
+                "point holds %zu (use fgmm_em_fused with a caller workspace)",
+                N, K, d, need, kScratchBytes);
+  void* ptr = nullptr;
+  if ((rc = scratch_address(&ptr))) return rc;
+  return em_fused_impl(X, mu, var, log_pi, N, K, d, variant, new_mu, new_var, new_log_pi,
+                       log_normalizer, ptr, kScratchBytes, stream);
 }
 
 int fgmm_log_normalizer(const float* X, const float* mu, const float* var,

@@ -105,6 +105,24 @@ int fgmm_em_fused(const float* X, const float* mu, const float* var,
                   float* log_normalizer, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * fgmm_em_fused without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Its scratch is a static device array of the library,
+ * fgmm_em_fused_noalloc_max_bytes() = 64 MiB on each GPU it runs on, held
+ * until the process ends; problems whose fgmm_workspace_bytes exceed it are
+ * rejected with FGMM_EWORKSPACE before any device work.  The call allocates
+ * nothing (no hipMalloc / hipFree).  Results equal fgmm_em_fused's.  Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (different streams or threads, not ordered by the caller) race.
+ */
+size_t fgmm_em_fused_noalloc_max_bytes(void);
+int fgmm_em_fused_noalloc(const float* X, const float* mu, const float* var,
+                          const float* log_pi, long N, int K, int d, int variant,
+                          float* new_mu, float* new_var, float* new_log_pi,
+                          float* log_normalizer, void* stream);
+
+/*
  * Pass 1 alone: log_normalizer[n] = logsumexp_k(log pi_k + log N(x_n|mu_k,var_k)).
  * Replaces flash_log_normalizer_v2_kernel (flash_gmm/csrc/flash_gmm_cuda.cu:72-170);
  * the Python reference splits the same stage out as the first half of
