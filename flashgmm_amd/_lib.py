@@ -50,7 +50,21 @@ SIGNATURES = {
     "fgmm_profile_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)], _I),
 }
 
+# host path (include/flashgmm_cpu.h): host pointers, synchronous, OpenMP
+CPU_LIB_PATH = os.path.join(PKG, "libflashgmm_cpu.so")
+CPU_SIGNATURES = {
+    "fgmm_cpu_last_error": ([], ctypes.c_char_p),
+    "fgmm_cpu_em_fused": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _P], _I),
+    "fgmm_cpu_log_normalizer": ([_P, _P, _P, _P, _L, _I, _I, _I, _P], _I),
+    "fgmm_cpu_accumulate_stats": ([_P, _P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P], _I),
+    "fgmm_cpu_m_step_update": ([_P, _P, _P, _L, _I, _I, _P, _P, _P], _I),
+    "fgmm_cpu_e_step": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P], _I),
+    "fgmm_cpu_standard_m_step": ([_P, _P, _L, _I, _I, _I, _P, _P, _P], _I),
+    "fgmm_cpu_em_fit": ([_P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _P, _P, _P], _I),
+}
+
 _lib = None
+_cpu = None
 _lock = threading.Lock()
 
 
@@ -72,6 +86,33 @@ def load(path: str | None = None):
     if path is None:
         _lib = lib
     return lib
+
+
+def load_cpu(path: str | None = None):
+    """Load and type the host-path library once; raises RuntimeError if it is
+    absent (there is no Python fallback)."""
+    global _cpu
+    if _cpu is not None and path is None:
+        return _cpu
+    p = path or CPU_LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(
+            f"flashgmm_amd: host library not found at {p}; build it with "
+            "`python -m flashgmm_amd.build`")
+    lib = ctypes.CDLL(p)
+    for name, (args, res) in CPU_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if path is None:
+        _cpu = lib
+    return lib
+
+
+def check_cpu(rc: int) -> None:
+    if rc != FGMM_OK:
+        msg = load_cpu().fgmm_cpu_last_error().decode(errors="replace")
+        raise RuntimeError(f"flashgmm_amd (host): {msg} (code {rc})")
 
 
 def check(rc: int) -> None:

@@ -1,4 +1,5 @@
-"""Builds ``flashgmm_amd/libflashgmm.so`` (hipcc, gfx950) in-tree.
+"""Builds ``flashgmm_amd/libflashgmm.so`` (hipcc, gfx950) and the host path
+``flashgmm_amd/libflashgmm_cpu.so`` (g++, OpenMP) in-tree.
 
 Usage: ``python -m flashgmm_amd.build`` (or ``__graft_entry__.build()``).
 Each ``csrc/*.hip`` translation unit is compiled to an object under
@@ -50,7 +51,33 @@ def _compile(src: str) -> str:
     return obj
 
 
+# The host path (CPU tensors): plain C++ with OpenMP, no HIP.  AVX2 + FMA is
+# the vector baseline of every x86-64 host these boxes use.
+CPU_SRC = os.path.join(CSRC, "cpu", "fgmm_cpu.cpp")
+CPU_OUT = os.path.join(PKG, "libflashgmm_cpu.so")
+CPU_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-mavx2", "-mfma", "-Wall",
+             "-I", os.path.join(ROOT, "include")]
+
+
+def build_cpu(verbose: bool = True) -> str:
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("g++ not found (needed for libflashgmm_cpu.so)")
+    tmp = CPU_OUT + ".tmp"
+    cmd = [cxx, *CPU_FLAGS, CPU_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed:\n{' '.join(cmd)}\n{r.stderr}")
+    if r.stderr.strip():
+        sys.stderr.write(r.stderr + "\n")
+    os.replace(tmp, CPU_OUT)
+    if verbose:
+        print(f"[flashgmm_amd] built {CPU_OUT}")
+    return CPU_OUT
+
+
 def build(verbose: bool = True) -> str:
+    build_cpu(verbose)
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))

@@ -4,19 +4,23 @@ Same function names, argument order, defaults and return order as the
 reference's pybind11 module (``flash_gmm/csrc/binding.cpp:94-109``:
 ``standard_e_step``, ``flash_e_step``, ``flash_em_fused``, ``standard_m_step``),
 plus the three stage entry points (``flash_log_normalizer``,
-``flash_accumulate_stats``, ``m_step_update``) and the device-resident loop
-``em_fit``.  Every call goes to ``libflashgmm.so`` (hand-written HIP
-kernels for gfx950) on torch's current stream; tensors must live on a ROCm
-device.  Outputs are fresh tensors; inputs are never modified.
+``flash_accumulate_stats``, ``m_step_update``) and the iteration loop
+``em_fit``.  Outputs are fresh tensors on the input's device; inputs are
+never modified.
+
+Dispatch on the device of X, as the reference's binding does
+(``binding.cpp:41-48,55-59,68-75,82-91``):
+  * ROCm tensors -> ``libflashgmm.so`` (hand-written HIP kernels for gfx950)
+    on torch's current stream;
+  * CPU tensors -> ``libflashgmm_cpu.so`` (this package's C++/OpenMP host
+    path, fp64 arithmetic, torch.get_num_threads() threads).
+Neither path falls back to the other or to Python: a missing library raises.
+Every other tensor argument must live on X's device.
 
 Errors are ``RuntimeError`` like the reference's ``TORCH_CHECK``; the dtype
 check keeps the reference's message ("X must be float32",
 ``binding.cpp:38,54,65,80``).  Unlike the reference, shapes, devices,
-``d <= 256`` and launch failures are checked too, before any device work.
-
-The reference dispatches CPU tensors to its OpenMP path
-(``binding.cpp:48,59,75,91``).  This module accelerates the ROCm path only and
-raises on CPU tensors instead of computing elsewhere.  Conversely the
+``d <= 256`` and launch failures are checked too, before any work.  The
 reference refuses ``flash_e_step`` on CUDA tensors (``binding.cpp:55-57``);
 here it runs on the device.
 """
@@ -32,10 +36,17 @@ def _ptr(t: torch.Tensor) -> int:
 
 
 def _check_device(X: torch.Tensor, fn: str) -> None:
-    if not X.is_cuda:
+    if not (X.is_cuda or X.device.type == "cpu"):
         raise RuntimeError(
-            f"flashgmm_amd.{fn}: tensors must be on a ROCm device (got {X.device}); "
-            "this module has no CPU implementation")
+            f"flashgmm_amd.{fn}: tensors must be on a ROCm device or the CPU (got {X.device})")
+
+
+def _on_host(X: torch.Tensor) -> bool:
+    return X.device.type == "cpu"
+
+
+def _threads() -> int:
+    return max(1, torch.get_num_threads())
 
 
 def _params(X, mu, var, log_pi, fn):
@@ -85,13 +96,18 @@ def flash_em_fused(X, mu, var, log_pi, BN: int = 64, BK: int = 8, *, variant=Non
     if int(BN) < 1 or int(BK) < 1:
         raise RuntimeError(f"flashgmm_amd.flash_em_fused: BN and BK must be >= 1 (got {BN}, {BK})")
     X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, "flash_em_fused")
-    v = _lib.variant_code(variant)
-    lib = _lib.load()
-    ws, nbytes = _ws(X, N, K, d, v)
     new_mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
     new_var = torch.empty((K, d), dtype=torch.float32, device=X.device)
     new_log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
     ln = torch.empty((N,), dtype=torch.float32, device=X.device)
+    if _on_host(X):
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_em_fused(
+            _ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, _threads(), _ptr(new_mu),
+            _ptr(new_var), _ptr(new_log_pi), _ptr(ln)))
+        return [new_mu, new_var, new_log_pi, ln]
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
     _lib.check(lib.fgmm_em_fused(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, v,
                                  _ptr(new_mu), _ptr(new_var), _ptr(new_log_pi), _ptr(ln),
                                  _ptr(ws), nbytes, _lib.stream_handle(X.device)))
@@ -102,10 +118,14 @@ def flash_log_normalizer(X, mu, var, log_pi, *, variant=None):
     """Pass 1: ``log_normalizer[n] = logsumexp_k(log pi_k + log N(x_n | mu_k, var_k))``
     (``flash_gmm_cuda.cu:72-170``; ``flash_e_step.py:144-177``)."""
     X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, "flash_log_normalizer")
+    ln = torch.empty((N,), dtype=torch.float32, device=X.device)
+    if _on_host(X):
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_log_normalizer(
+            _ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, _threads(), _ptr(ln)))
+        return ln
     v = _lib.variant_code(variant)
     lib = _lib.load()
     ws, nbytes = _ws(X, N, K, d, v)
-    ln = torch.empty((N,), dtype=torch.float32, device=X.device)
     _lib.check(lib.fgmm_log_normalizer(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, v,
                                        _ptr(ln), _ptr(ws), nbytes,
                                        _lib.stream_handle(X.device)))
@@ -124,12 +144,17 @@ def flash_accumulate_stats(X, mu, var, log_pi, log_normalizer, *, variant=None):
         raise RuntimeError("flashgmm_amd.flash_accumulate_stats: log_normalizer is on "
                            f"{log_normalizer.device}, X on {X.device}")
     ln = log_normalizer.contiguous()
-    v = _lib.variant_code(variant)
-    lib = _lib.load()
-    ws, nbytes = _ws(X, N, K, d, v)
     n_k = torch.empty((K,), dtype=torch.float32, device=X.device)
     s_k = torch.empty((K, d), dtype=torch.float32, device=X.device)
     sq_k = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    if _on_host(X):
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_accumulate_stats(
+            _ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(ln), N, K, d, _threads(),
+            _ptr(n_k), _ptr(s_k), _ptr(sq_k)))
+        return [n_k, s_k, sq_k]
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
     _lib.check(lib.fgmm_accumulate_stats(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(ln),
                                          N, K, d, v, _ptr(n_k), _ptr(s_k), _ptr(sq_k),
                                          _ptr(ws), nbytes, _lib.stream_handle(X.device)))
@@ -138,10 +163,16 @@ def flash_accumulate_stats(X, mu, var, log_pi, log_normalizer, *, variant=None):
 
 def _gamma_estep(X, mu, var, log_pi, variant, fn, standard):
     X, mu, var, log_pi, N, K, d = _params(X, mu, var, log_pi, fn)
-    v = _lib.variant_code(variant)
-    lib = _lib.load()
     gamma = torch.empty((N, K), dtype=torch.float32, device=X.device)
     ln = torch.empty((N,), dtype=torch.float32, device=X.device)
+    if _on_host(X):
+        # standard and flash E-steps return the same quantities on the host
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_e_step(
+            _ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, _threads(), _ptr(gamma),
+            _ptr(ln)))
+        return [gamma, ln]
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
     stream = _lib.stream_handle(X.device)
     if standard:
         # the N x K fp64 matrix lives only for this call, like the reference's L
@@ -202,14 +233,18 @@ def standard_m_step(X, gamma):
                            f"X on {X.device}")
     K = gamma.shape[1]
     X, gamma = X.contiguous(), gamma.contiguous()
+    mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    var = torch.empty((K, d), dtype=torch.float32, device=X.device)
+    log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
+    if _on_host(X):
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_standard_m_step(
+            _ptr(X), _ptr(gamma), N, K, d, _threads(), _ptr(mu), _ptr(var), _ptr(log_pi)))
+        return [mu, var, log_pi]
     lib = _lib.load()
     nbytes = lib.fgmm_standard_m_step_workspace_bytes(N, K, d)
     if nbytes == 0:
         raise RuntimeError("flashgmm_amd: " + lib.fgmm_last_error().decode(errors="replace"))
     ws = _lib.workspace(X.device, nbytes)
-    mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
-    var = torch.empty((K, d), dtype=torch.float32, device=X.device)
-    log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
     _lib.check(lib.fgmm_standard_m_step(_ptr(X), _ptr(gamma), N, K, d, _ptr(mu), _ptr(var),
                                         _ptr(log_pi), _ptr(ws), nbytes,
                                         _lib.stream_handle(X.device)))
@@ -233,13 +268,17 @@ def m_step_update(n_k, s_k, sq_k, N: int):
     N = int(N)
     if N < 1:
         raise RuntimeError("flashgmm_amd.m_step_update: N must be >= 1")
-    lib = _lib.load()
     # the contiguous copies stay bound until the call has been queued: a
     # temporary freed earlier could hand its block to the next copy
     n_c, s_c, sq_c = n_k.contiguous(), s_k.contiguous(), sq_k.contiguous()
     mu = torch.empty((K, d), dtype=torch.float32, device=s_k.device)
     var = torch.empty((K, d), dtype=torch.float32, device=s_k.device)
     log_pi = torch.empty((K,), dtype=torch.float32, device=s_k.device)
+    if _on_host(s_k):
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_m_step_update(
+            _ptr(n_c), _ptr(s_c), _ptr(sq_c), N, K, d, _ptr(mu), _ptr(var), _ptr(log_pi)))
+        return [mu, var, log_pi]
+    lib = _lib.load()
     _lib.check(lib.fgmm_m_step_update(_ptr(n_c), _ptr(s_c), _ptr(sq_c), N, K, d, _ptr(mu),
                                       _ptr(var), _ptr(log_pi), _lib.stream_handle(s_k.device)))
     return [mu, var, log_pi]
@@ -256,13 +295,18 @@ def em_fit(X, mu0, var0, log_pi0, iters: int, *, variant=None):
     iters = int(iters)
     if iters < 1:
         raise RuntimeError("flashgmm_amd.em_fit: iters must be >= 1")
-    v = _lib.variant_code(variant)
-    lib = _lib.load()
-    ws, nbytes = _ws(X, N, K, d, v)
     mu = torch.empty((K, d), dtype=torch.float32, device=X.device)
     var = torch.empty((K, d), dtype=torch.float32, device=X.device)
     log_pi = torch.empty((K,), dtype=torch.float32, device=X.device)
     traj = torch.empty((iters,), dtype=torch.float64, device=X.device)
+    if _on_host(X):
+        _lib.check_cpu(_lib.load_cpu().fgmm_cpu_em_fit(
+            _ptr(X), _ptr(mu0), _ptr(var0), _ptr(log_pi0), N, K, d, iters, _threads(),
+            _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(traj)))
+        return mu, var, log_pi, traj
+    v = _lib.variant_code(variant)
+    lib = _lib.load()
+    ws, nbytes = _ws(X, N, K, d, v)
     _lib.check(lib.fgmm_em_fit(_ptr(X), _ptr(mu0), _ptr(var0), _ptr(log_pi0), N, K, d, iters, v,
                                _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(traj), _ptr(ws), nbytes,
                                _lib.stream_handle(X.device)))

@@ -124,7 +124,8 @@ class NativeFlashGMM:
             self._init_params(X)
         else:
             self.mu, self.var, self.log_pi = (t.to(X.device, torch.float32) for t in init)
-        torch.cuda.synchronize(X.device)
+        if X.is_cuda:
+            torch.cuda.synchronize(X.device)
         t0 = time.time()
         self.mu, self.var, self.log_pi, traj = _C.em_fit(X, self.mu, self.var, self.log_pi,
                                                          n_iter)

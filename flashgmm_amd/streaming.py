@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .flash_gmm_native import _check_device, _ptr
+from .flash_gmm_native import _ptr
 
 
 class StreamingFlashGMM:
@@ -39,7 +39,9 @@ class StreamingFlashGMM:
             raise RuntimeError("X must be float32")
         if X.dim() != 2:
             raise RuntimeError("X must be 2D")
-        _check_device(mu, "StreamingFlashGMM.em_step")
+        if not mu.is_cuda:   # X may live on the host; the iteration runs on the device
+            raise RuntimeError("flashgmm_amd.StreamingFlashGMM.em_step: mu/var/log_pi must be "
+                               f"on a ROCm device (got {mu.device})")
         N, d = X.shape
         K = mu.shape[0]
         if N < 1 or d < 1 or d > 256:

@@ -135,6 +135,9 @@ def test_argument_errors_before_device_work(lib):
 
 
 def test_python_errors_mirror_reference():
+    """The reference's TORCH_CHECKs (binding.cpp:38-39,54,65,80) and this
+    module's extra checks raise RuntimeError before any work; CPU tensors are
+    served by the host path (tests/test_cpu_path.py), other devices refused."""
     import torch
     from flashgmm_amd import flash_gmm_native as C
     X = torch.zeros(10, 4)
@@ -143,19 +146,19 @@ def test_python_errors_mirror_reference():
         C.flash_em_fused(X.double(), mu, var, lp)
     with pytest.raises(RuntimeError, match="X must be 2D"):
         C.flash_log_normalizer(X[0], mu, var, lp)
-    with pytest.raises(RuntimeError, match="ROCm device"):
-        C.flash_em_fused(X, mu, var, lp)
+    with pytest.raises(RuntimeError, match="ROCm device or the CPU"):
+        C.flash_em_fused(X.to("meta"), mu.to("meta"), var.to("meta"), lp.to("meta"))
     with pytest.raises(RuntimeError, match="BN and BK"):
         C.flash_em_fused(X, mu, var, lp, 0, 8)
     for fn in (C.standard_e_step, C.flash_e_step):
         with pytest.raises(RuntimeError, match="X must be float32"):
             fn(X.double(), mu, var, lp)
-        with pytest.raises(RuntimeError, match="ROCm device"):
-            fn(X, mu, var, lp)
+        with pytest.raises(RuntimeError, match="log_pi must be"):
+            fn(X, mu, var, lp[:1])
     with pytest.raises(RuntimeError, match="X must be float32"):
         C.standard_m_step(X.double(), torch.zeros(10, 2))
-    with pytest.raises(RuntimeError, match="ROCm device"):
-        C.standard_m_step(X, torch.zeros(10, 2))
+    with pytest.raises(RuntimeError, match="gamma must be"):
+        C.standard_m_step(X, torch.zeros(9, 2))
     with pytest.raises(RuntimeError, match="BK must be"):
         C.flash_e_step(X, mu, var, lp, BK=0)
     with pytest.raises(RuntimeError, match="unknown variant"):
