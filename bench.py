@@ -108,6 +108,8 @@ def arithmetic_type(variant: str) -> str:
     if variant in ("mfma", "mixed"):
         return ("f64 matrix cores (distance, sum gamma x^2, reduction) + f32 (gamma, sum gamma x)"
                 + (" + f32 matrix-core Pass-1 bound sweep" if variant == "mixed" else ""))
+    if variant == "small":
+        return "f64 (vector ALU; every stage of an iteration in one launch)"
     return "f64 (vector ALU)"
 
 
@@ -133,6 +135,8 @@ def pass_work(cfg, variant, which):
     the fp64 vector ALU."""
     N = float(cfg.N)
     Kp, dp, dpb = padded(cfg, variant)
+    if variant == "small":   # one launch: distance (4) + statistics (4) per (n, k, j), fp64
+        return 8.0 * N * cfg.K * cfg.d, FP64_PEAK, "fp64 vector ALU, one launch per iteration"
     if variant == "valu":
         f = (4.0 if which == 1 else 8.0) * N * cfg.K * cfg.d
         return f, FP64_PEAK, "fp64 vector ALU"
@@ -159,10 +163,11 @@ def dominant_roofline(cfg, variant, kernels):
     nkd = float(cfg.N) * cfg.K * cfg.d
     t1 = kernels["pass1"]["ms_avg"] / 1e3
     t2 = kernels["pass2"]["ms_avg"] / 1e3
-    which = 1 if (variant == "sparse" or t1 >= t2) else 2
+    which = 1 if (variant in ("sparse", "small") or t1 >= t2) else 2
     t = t1 if which == 1 else t2
     issued, peak, unit = pass_work(cfg, variant, which)
-    name = ("pass1 (log-normalizer sweep" if which == 1
+    name = ("fused iteration (all stages" if variant == "small"
+            else "pass1 (log-normalizer sweep" if which == 1
             else "pass2 (gamma recompute + sufficient statistics")
     achieved = issued / t if t > 0 else 0.0
     out = {"kernel": f"{name}, {unit})", "bound": "mfma", "achieved": achieved / 1e12,
@@ -197,6 +202,10 @@ def work_model(cfg, variant, ms_per_step, counts):
         parts = {"bf16_sweep_us": t_mfma * 1e6, "fp64_us": t_f64 * 1e6,
                  "listed_entries": int(E), "flagged_components": int(flagged)}
         t_c = t_mfma + t_f64
+    elif variant == "small":
+        f1, p1, _ = pass_work(cfg, variant, 1)
+        t_c = f1 / p1
+        parts = {"fused_us": t_c * 1e6}
     else:
         f1, p1, _ = pass_work(cfg, variant, 1)
         f2, p2, _ = pass_work(cfg, variant, 2)

@@ -17,7 +17,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libflashgmm.so")
 
 FGMM_OK, FGMM_EINVAL, FGMM_EWORKSPACE, FGMM_EHIP = 0, 1, 2, 3
-VARIANTS = {"auto": 0, "valu": 1, "mfma": 2, "x32": 3, "mixed": 4, "sparse": 5}
+VARIANTS = {"auto": 0, "valu": 1, "mfma": 2, "x32": 3, "mixed": 4, "sparse": 5, "small": 6}
 
 # name -> (argtypes, restype); mirrors include/flashgmm.h
 _P, _L, _I, _Z = ctypes.c_void_p, ctypes.c_long, ctypes.c_int, ctypes.c_size_t

@@ -22,7 +22,7 @@ BUILD = os.path.join(PKG, "_build")
 ARCH = os.environ.get("FLASH_GMM_HIP_ARCH", "gfx950")
 
 SOURCES = ["fgmm_api.hip", "fgmm_common.hip", "fgmm_mfma.hip", "fgmm_valu.hip", "fgmm_x32.hip",
-           "fgmm_resp.hip", "fgmm_sparse.hip"]
+           "fgmm_resp.hip", "fgmm_sparse.hip", "fgmm_small.hip"]
 
 # Packed-fp32 VALU forms are disabled for all device code (the compiler would
 # otherwise form v_pk_* fp32 ops from plain float code).

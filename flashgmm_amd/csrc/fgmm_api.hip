@@ -44,8 +44,17 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // pairs, statistics from those lists) beats the dense fp64 Pass 2 by
 // 1.1x (K = 128) to 2.5x (K = 512, N = 2^20) at d = 64 and 128 (measured);
 // it needs N * min(K, 32) < 2^31 and K <= 8192.
+// The small variant (one launch per iteration) when the whole problem is a
+// few workgroups and its merge of their partial rows stays small.
+static bool small_fits(long N, int K, int d) {
+  if (K > kSmallMaxK || d > kSmallMaxD || N > 16384) return false;
+  const long G = (N + small_points(K, d) - 1) / small_points(K, d);
+  return G * K * (2L * d + 1) <= 65536;
+}
+
 static int resolve_variant(long N, int K, int d, int variant) {
-  if (variant >= kValu && variant <= kSparse) return variant;
+  if (variant >= kValu && variant <= kLastVariant) return variant;
+  if (small_fits(N, K, d)) return kSmall;
   if (d <= 128 && K >= 128 && K <= 8192 && N * (long)(K < kSpCap ? K : kSpCap) < 2147483647L)
     return kSparse;
   if (d <= 128 && K >= 256) return kMixed;
@@ -59,6 +68,20 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.K = K;
   g.d = d;
   g.variant = resolve_variant(N, K, d, variant);
+  if (g.variant == kSmall) {
+    g.dp = d;
+    g.Kp = K;
+    const int P = small_points(K, d);
+    g.p1_blocks = (int)((N + P - 1) / P);
+    g.p2_kblocks = 1;
+    g.p2_chunks = g.p1_blocks;
+    g.p2_chunk = P;
+    g.stat_w = 2 * d + 1;
+    g.sp_C = 0;
+    g.sp_chunk = 0;
+    g.sp_nchunk = 0;
+    return g;
+  }
   if (g.variant == kMfma || g.variant == kX32 || both_sets(g.variant)) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
@@ -166,6 +189,14 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
 WsLayout make_layout(const Geom& g) {
   WsLayout L;
   size_t off = 0;
+  if (g.variant == kSmall) {   // counter, per-workgroup sums of ln, partial rows
+    L.aux = 0;
+    L.lnsum = 256;
+    L.part = align256(L.lnsum + sizeof(double) * (size_t)g.p1_blocks);
+    L.total = align256(L.part + sizeof(double) * (size_t)g.p2_chunks * g.K * g.stat_w);
+    L.params = L.bias = L.ln2 = L.total;
+    return L;
+  }
   const bool x32 = g.variant == kX32;
   const bool both = both_sets(g.variant);
   const bool xset = x32 || both;                       // holds the x32 coefficient set
@@ -247,8 +278,11 @@ static int validate_shape(long N, int K, int d, int variant) {
   if (K > 65536) return fail(FGMM_EINVAL, "K must be <= 65536 (got %d)", K);
   if (d < 1 || d > kMaxD)
     return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
-  if (variant < 0 || variant > kSparse)
+  if (variant < 0 || variant > kLastVariant)
     return fail(FGMM_EINVAL, "unknown variant %d", variant);
+  if (variant == kSmall && (K > kSmallMaxK || d > kSmallMaxD))
+    return fail(FGMM_EINVAL, "the small variant supports K <= %d and d <= %d (got K=%d, d=%d)",
+                kSmallMaxK, kSmallMaxD, K, d);
   if (variant == kSparse && (d > 128 || K > 8192))
     return fail(FGMM_EINVAL, "the sparse variant supports d <= 128 and K <= 8192 (got d=%d, K=%d)",
                 d, K);
@@ -326,6 +360,21 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
   if (g.variant == kSparse)
     w.layout_ok = sparse_aux(g, b, L.aux, &w.x, &w.sp) == L.total;
   return w;
+}
+
+// Small variant: the arrival counter at the workspace's start, and one
+// fused iteration (timed as Pass 1: the launch holds every stage).
+static unsigned* small_counter(void* ws, const WsLayout& L) {
+  return reinterpret_cast<unsigned*>(static_cast<char*>(ws) + L.aux);
+}
+static int run_small(const Geom& g, const float* X, Ws& w, unsigned* counter,
+                     const float* mu_in, const float* var_in, const float* lp_in,
+                     float* mu_out, float* var_out, float* lp_out, float* ln_out,
+                     double* ll_out, hipStream_t s) {
+  Timed t(1, s);
+  return check_hip(launch_em_small(g, X, mu_in, var_in, lp_in, mu_out, var_out, lp_out, ln_out,
+                                   w.part, w.lnsum, counter, ll_out, s),
+                   "fused iteration (small)");
 }
 
 // Reduction + M-step of one iteration.  x32: stage 1 reduces the components
@@ -408,8 +457,9 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
 // candidate scheme would pay off only when gamma is consumed on chip, and
 // Pass 2 from a caller's log-normalizer) run the fp64 matrix-core path.
 static int estep_variant(int K, int d, int variant) {
-  if (variant < 0 || variant > kSparse) return variant;   // rejected by validate_shape
-  variant = resolve_variant(1, K, d, variant);   // N only decides sparse vs mixed
+  if (variant < 0 || variant > kLastVariant) return variant;   // rejected by validate_shape
+  variant = resolve_variant(1L << 40, K, d, variant);   // N only decides sparse / mixed / small
+  if (variant == kSmall) return (d <= 128 && K >= 8) ? kMfma : kValu;
   return (variant == kX32 || both_sets(variant)) ? kMfma : variant;
 }
 
@@ -445,8 +495,9 @@ static size_t stream_acc_bytes(const Geom& g) {
   return align256(sizeof(double) * ((size_t)g.Kp * g.stat_w + 1));
 }
 static int stream_variant(int K, int d, int variant) {
-  if (variant < 0 || variant > kSparse) return variant;   // rejected by validate_shape
-  variant = resolve_variant(1, K, d, variant);
+  if (variant < 0 || variant > kLastVariant) return variant;   // rejected by validate_shape
+  variant = resolve_variant(1L << 40, K, d, variant);
+  if (variant == kSmall) variant = (d <= 128 && K >= 8) ? kMfma : kValu;
   if (variant == kSparse) variant = K >= 256 ? kMixed : kMfma;
   return variant == kX32 ? kMfma : variant;
 }
@@ -494,6 +545,12 @@ static int em_fused_impl(const float* X, const float* mu, const float* var,
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   Ws w = carve(g, ws, L);
+  if (g.variant == kSmall) {
+    if ((rc = check_hip(launch_small_reset(small_counter(ws, L), s), "counter reset")))
+      return rc;
+    return run_small(g, X, w, small_counter(ws, L), mu, var, log_pi, new_mu, new_var, new_log_pi,
+                     log_normalizer, nullptr, s);
+  }
   if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
   if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
   if ((rc = run_pass2(g, X, w, s))) return rc;
@@ -552,7 +609,11 @@ int fgmm_workspace_region(long N, int K, int d, int variant, const char* name,
 
 size_t fgmm_workspace_bytes(long N, int K, int d, int variant) {
   if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
-  return make_layout(make_geom(N, K, d, variant)).total;
+  const size_t own = make_layout(make_geom(N, K, d, variant)).total;
+  if (resolve_variant(N, K, d, variant) != kSmall) return own;
+  // the stage entry points run the dense kernels for a small problem
+  const size_t dense = make_layout(make_geom(N, K, d, estep_variant(K, d, kSmall))).total;
+  return own > dense ? own : dense;
 }
 
 int fgmm_em_fused(const float* X, const float* mu, const float* var, const float* log_pi,
@@ -598,6 +659,10 @@ int fgmm_log_normalizer(const float* X, const float* mu, const float* var,
                         float* log_normalizer, void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
   int rc = validate_shape(N, K, d, variant);
+  if (rc) return rc;
+  // the small variant fuses every stage; Pass 1 alone runs the dense kernels
+  if (resolve_variant(N, K, d, variant) == kSmall) variant = estep_variant(K, d, kSmall);
+  rc = validate_shape(N, K, d, variant);
   if (rc) return rc;
   FGMM_REQUIRE(X); FGMM_REQUIRE(mu); FGMM_REQUIRE(var); FGMM_REQUIRE(log_pi);
   FGMM_REQUIRE(log_normalizer);
@@ -666,6 +731,18 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
   if ((rc = validate_ws(g, L, ws, ws_bytes))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   Ws w = carve(g, ws, L);
+  if (g.variant == kSmall) {   // one launch per iteration, parameters in the outputs
+    unsigned* ctr = small_counter(ws, L);
+    if ((rc = check_hip(launch_small_reset(ctr, s), "counter reset"))) return rc;
+    for (int it = 0; it < iters; it++) {
+      const bool first = it == 0;
+      rc = run_small(g, X, w, ctr, first ? mu0 : mu_out, first ? var0 : var_out,
+                     first ? log_pi0 : log_pi_out, mu_out, var_out, log_pi_out, nullptr,
+                     ll_traj + it, s);
+      if (rc) return rc;
+    }
+    return FGMM_OK;
+  }
   if ((rc = run_precompute(g, mu0, var0, log_pi0, w, s))) return rc;
   for (int it = 0; it < iters; it++) {
     if ((rc = run_pass1(g, X, w, nullptr, s))) return rc;

@@ -32,7 +32,19 @@ inline long round_up_l(long x, long m) { return (x + m - 1) / m * m; }
 // candidates) with the fp64 matrix-core Pass 2 (no slots, no guard needed).
 // kSparse: the x32 Pass 1 also lists every exactly evaluated pair per point;
 // Pass 2 accumulates the statistics from those lists alone (fgmm_sparse.hip).
-enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3, kMixed = 4, kSparse = 5 };
+// kSmall: one launch per iteration (fgmm_small.hip) for K <= 32, d <= 64.
+enum Variant : int { kAuto = 0, kValu = 1, kMfma = 2, kX32 = 3, kMixed = 4, kSparse = 5,
+                     kSmall = 6, kLastVariant = kSmall };
+constexpr int kSmallThreads = 1024;   // threads per workgroup of the small variant
+constexpr int kSmallMaxK = 32;
+constexpr int kSmallMaxD = 64;
+constexpr size_t kSmallMaxLds = 159 * 1024;   // gfx950: 160 KiB of LDS per workgroup, less static
+// LDS of one small-variant workgroup of P points (fgmm_small.hip).
+size_t small_lds_bytes(int K, int d, int P);
+// Points per small-variant workgroup: 256, or 128 when 256 would not fit.
+inline int small_points(int K, int d) {
+  return small_lds_bytes(K, d, 256) <= kSmallMaxLds ? 256 : 128;
+}
 // Variants that keep both the fp64 fragment-ordered coefficient set and the
 // x32 set behind it.
 __host__ __device__ inline bool both_sets(int v) { return v == kMixed || v == kSparse; }
@@ -291,6 +303,14 @@ hipError_t launch_lse_rows(long N, int K, const double* Lmat, float* gamma,
 // Pass-2 partial layout of g (g describes an MFMA geometry; d <= 256).
 hipError_t launch_gamma_stats(const Geom& g, const float* X, const float* gamma,
                               double* part, hipStream_t s);
+// Small variant: one fused iteration per launch (fgmm_small.hip).  `counter`
+// must be 0 before the first launch (launch_small_reset); each launch leaves
+// it 0.  mu_in/var_in/lp_in may alias mu_out/var_out/lp_out.
+hipError_t launch_em_small(const Geom& g, const float* X, const float* mu_in,
+                           const float* var_in, const float* lp_in, float* mu_out,
+                           float* var_out, float* lp_out, float* ln_out, double* part,
+                           double* lnsum, unsigned* counter, double* ll_out, hipStream_t s);
+hipError_t launch_small_reset(unsigned* counter, hipStream_t s);
 hipError_t launch_pass1_x32(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                             float* ln_out, double* lnsum, hipStream_t s);
 hipError_t launch_pass2_x32(const Geom& g, const float* X, const X32Ws& w,

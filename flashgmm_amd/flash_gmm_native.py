@@ -316,4 +316,4 @@ def em_fit(X, mu0, var0, log_pi0, iters: int, *, variant=None):
 def resolve_variant(N: int, K: int, d: int, variant=None) -> str:
     """Name of the kernel family the library runs for this shape."""
     code = _lib.load().fgmm_resolve_variant(int(N), int(K), int(d), _lib.variant_code(variant))
-    return {1: "valu", 2: "mfma", 3: "x32", 4: "mixed", 5: "sparse"}[code]
+    return {1: "valu", 2: "mfma", 3: "x32", 4: "mixed", 5: "sparse", 6: "small"}[code]

@@ -54,8 +54,12 @@ def test_version_and_variant_table(lib):
     assert lib.fgmm_resolve_variant(4096, 64, 32, 0) == 2
     assert lib.fgmm_resolve_variant(65536, 9000, 64, 0) == 4        # K > 8192: mixed
     assert lib.fgmm_resolve_variant(1 << 27, 256, 64, 0) == 4       # N * 32 >= 2^31
-    assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 2
-    assert lib.fgmm_resolve_variant(4096, 7, 32, 0) == 1
+    assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 6          # small: one launch
+    assert lib.fgmm_resolve_variant(4096, 7, 32, 0) == 6
+    assert lib.fgmm_resolve_variant(65536, 8, 32, 0) == 2         # too many workgroups
+    assert lib.fgmm_resolve_variant(65536, 7, 32, 0) == 1
+    assert lib.fgmm_resolve_variant(4096, 33, 32, 0) == 2         # K > 32
+    assert lib.fgmm_resolve_variant(4096, 8, 65, 0) == 2          # d > 64
     assert lib.fgmm_resolve_variant(4096, 64, 200, 0) == 1
     assert lib.fgmm_resolve_variant(4096, 8, 32, 1) == 1          # forced vector ALU
 
@@ -120,10 +124,12 @@ def test_argument_errors_before_device_work(lib):
     assert _em(lib, d=0) == 1 and b"d must be" in lib.fgmm_last_error()
     assert _em(lib, d=257) == 1 and b"d must be" in lib.fgmm_last_error()
     assert _em(lib, d=200, variant=2) == 1 and b"MFMA" in lib.fgmm_last_error()
-    assert _em(lib, variant=7) == 1 and b"variant" in lib.fgmm_last_error()
+    assert _em(lib, variant=9) == 1 and b"variant" in lib.fgmm_last_error()
     assert _em(lib, d=200, variant=4) == 1 and b"mixed" in lib.fgmm_last_error()
     assert _em(lib, d=200, variant=5) == 1 and b"sparse" in lib.fgmm_last_error()
     assert _em(lib, K=8193, variant=5) == 1 and b"sparse" in lib.fgmm_last_error()
+    assert _em(lib, K=33, variant=6) == 1 and b"small" in lib.fgmm_last_error()
+    assert _em(lib, d=65, variant=6) == 1 and b"small" in lib.fgmm_last_error()
     for i in range(8):
         assert _em(lib, null=i) == 1 and b"must not be NULL" in lib.fgmm_last_error()
     assert _em(lib, ws=None) == 2 and b"NULL" in lib.fgmm_last_error()

@@ -27,6 +27,8 @@ def variants_for(K, d):
     v = ["valu"]
     if d <= 128:
         v += ["mfma", "x32", "mixed", "sparse"]
+    if K <= 32 and d <= 64:
+        v += ["small"]
     return v
 
 
@@ -124,7 +126,7 @@ def test_golden_vectors(cuda, name):
     with np.load(path, allow_pickle=False) as z:
         g = {k: z[k] for k in z.files}
     t = to_dev(cuda, g["X"], g["mu"], g["var"], g["log_pi"])
-    for variant in ("valu", "mfma", "x32", "mixed", "sparse"):
+    for variant in ("valu", "mfma", "x32", "mixed", "sparse", "small"):
         print(f"[case] golden {name} variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant=variant)]
         check_ln(out[3], g["ln"], f"{name} {variant}")
@@ -342,7 +344,7 @@ def test_unaligned_and_noncontiguous_inputs(cuda):
     Xu = big[1:].view(X.shape)                    # 4-byte offset: scalar load path
     assert Xu.data_ptr() % 16 != 0
     t = to_dev(cuda, mu, var, lp)
-    for variant in ("valu", "mfma", "x32", "mixed", "sparse"):
+    for variant in ("valu", "mfma", "x32", "mixed", "sparse", "small"):
         print(f"[case] unaligned X variant={variant}", flush=True)
         out = [o.cpu().numpy() for o in C.flash_em_fused(Xu, *t, variant=variant)]
         check_params(out[:3], ref[:3], f"unaligned {variant}")
@@ -509,3 +511,27 @@ def test_sparse_component_with_folded_pieces(cuda):
     b = C.flash_em_fused(*t, variant="sparse")
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("N,K,d", [(1000, 32, 64), (16384, 3, 5), (300, 1, 1), (2000, 31, 63)])
+def test_small_variant_extremes(cuda, N, K, d):
+    """The one-launch variant at its limits (K = 32 with d = 64, which takes
+    128-point workgroups; odd K and d; K = d = 1) against the fp64 oracle,
+    over a 3-iteration device loop too."""
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(N + K + d)
+    centers = rng.uniform(-4, 4, (K, d))
+    X = (centers[rng.integers(0, K, N)] + rng.normal(0, 1, (N, d))).astype(np.float32)
+    mu = (X[rng.choice(N, K, replace=False)]).astype(np.float32)
+    var = rng.uniform(0.5, 2.0, (K, d)).astype(np.float32)
+    lp = np.log(rng.dirichlet(np.ones(K))).astype(np.float32)
+    ref = O.c_em_fused(X, mu, var, lp)
+    t = to_dev(cuda, X, mu, var, lp)
+    print(f"[case] small extremes N={N} K={K} d={d}", flush=True)
+    out = [o.cpu().numpy() for o in C.flash_em_fused(*t, variant="small")]
+    check_ln(out[3], ref[3], f"small N={N} K={K} d={d}")
+    check_params(out[:3], ref[:3], f"small N={N} K={K} d={d}")
+    traj_ref, *_ = O.c_fit(X, mu, var, lp, 3)
+    _, _, _, traj = C.em_fit(*t, 3, variant="small")
+    e = np.abs(traj.cpu().numpy() - traj_ref) / np.abs(traj_ref)
+    assert e.max() <= 1e-4, e.max()
