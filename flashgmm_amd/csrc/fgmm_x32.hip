@@ -111,6 +111,16 @@ __device__ inline void load_octets32(const float* __restrict__ X, long n, long N
   }
 }
 
+// 1/v to fp64 accuracy (relative error a few ulp, not correctly rounded):
+// the hardware reciprocal estimate refined by one Newton step, which squares
+// its relative error.  Three fp64 operations against the ~10 of an IEEE
+// division.
+__device__ inline double recip_f64(double v) {
+  const double r = __builtin_amdgcn_rcp(v);
+  const double e = fma(-v, r, 1.0);
+  return fma(r, e, r);
+}
+
 __device__ inline void split_bf16(float v, __bf16& h, __bf16& l) {
   h = (__bf16)v;
   l = (__bf16)(v - (float)h);
@@ -295,7 +305,7 @@ __global__ __launch_bounds__(512) void pass1_x32_kernel(
           _Pragma("unroll") for (int i4_ = 0; i4_ < 4; i4_++) {                       \
             const float xv_ = __shfl(xq[4 * w_ + i4_], p_, 16);                       \
             const double t_ = (double)xv_ - (double)mv_[i4_];                         \
-            q_ += t_ * t_ / (double)vv_[i4_];                                         \
+            q_ = fma(t_ * t_, recip_f64((double)vv_[i4_]), q_);                       \
           }                                                                           \
         }                                                                             \
         q_ *= 0.5 * kLog2e;                                                           \
