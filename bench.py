@@ -233,7 +233,7 @@ def sparse_counts(lib, cfg, variant, ws):
             return {}
         view = ws[off.value:off.value + nb.value].view(torch.int32)
         if name == "pcnt":
-            cap = min(cfg.K, 32)
+            cap = min(cfg.K, 16)
             out["entries"] = int(view.clamp(max=cap).sum().item())
             out["overflow_points"] = int((view > cap).sum().item())
         else:

@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -43,7 +44,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // From K >= 128 the sparse variant (x32 Pass 1 listing each point's exact
 // pairs, statistics from those lists) beats the dense fp64 Pass 2 by
 // 1.1x (K = 128) to 2.5x (K = 512, N = 2^20) at d = 64 and 128 (measured);
-// it needs N * min(K, 32) < 2^31 and K <= 8192.
+// it needs N * min(K, 16) < 2^31 and K <= 8192.
 // The small variant (one launch per iteration) when the whole problem is a
 // few workgroups and its merge of their partial rows stays small.
 static bool small_fits(long N, int K, int d) {
@@ -80,6 +81,8 @@ Geom make_geom(long N, int K, int d, int variant) {
     g.sp_C = 0;
     g.sp_chunk = 0;
     g.sp_nchunk = 0;
+    g.sp_rows_fl = 0;
+    g.sp_ov_cap = 1;
     return g;
   }
   if (g.variant == kMfma || g.variant == kX32 || both_sets(g.variant)) {
@@ -118,6 +121,16 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.sp_C = K < kSpCap ? K : kSpCap;
   g.sp_chunk = kSpPts;
   g.sp_nchunk = (int)((N + kSpPts - 1) / kSpPts);
+  // dense fp64 passes of the sparse variant (sp_dense_rows): chunks of at
+  // most 16384 points; the flagged pass gets 8192 rows (about 512 work items
+  // however many components are flagged), the overflow pass a quarter of
+  // |X| (at least 8 MiB) of rows
+  const long min_chunks = (N + 16383) / 16384;
+  g.sp_rows_fl = (int)std::max<long>(8192, min_chunks * g.Kp);
+  const size_t row_set = sizeof(double) * (size_t)g.Kp * g.stat_w;
+  const size_t ov_bytes = std::max<size_t>(sizeof(float) * (size_t)N * d / 4, size_t(8) << 20);
+  g.sp_ov_cap = (int)std::min<long>(g.p2_chunks, std::max<long>(min_chunks, (long)(ov_bytes / row_set)));
+  if (g.sp_ov_cap < 1) g.sp_ov_cap = 1;
   return g;
 }
 
@@ -149,8 +162,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   char* glob = take(sizeof(double) * 4);
   char* sorted = take(sizeof(int2) * NC);
   char* prow = take(sizeof(double) * npc * (size_t)g.stat_w);
-  char* Xo = take(sizeof(float) * N * (size_t)g.d);
-  char* ln2o = take(sizeof(double) * N);
+  char* ovidx = take(sizeof(int) * N);
   char* kmap = take(sizeof(int) * Kp);
   char* nflag = take(sizeof(int));
   char* flag = take(sizeof(int) * Kp);
@@ -178,8 +190,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
     sp->glob = reinterpret_cast<double*>(glob);
     sp->sorted = reinterpret_cast<int2*>(sorted);
     sp->prow = reinterpret_cast<double*>(prow);
-    sp->Xo = reinterpret_cast<float*>(Xo);
-    sp->ln2o = reinterpret_cast<double*>(ln2o);
+    sp->ovidx = reinterpret_cast<int*>(ovidx);
     sp->kmap = reinterpret_cast<int*>(kmap);
     sp->nflag = reinterpret_cast<int*>(nflag);
   }
@@ -216,7 +227,11 @@ WsLayout make_layout(const Geom& g) {
   L.lnsum = off;
   off = align256(off + sizeof(double) * (size_t)g.p1_blocks);
   L.part = off;
-  off = align256(off + sizeof(double) * (size_t)g.p2_chunks * g.Kp * g.stat_w);
+  // sparse: the dense passes' rows, sized by sp_dense_rows (device counts
+  // decide how they are laid out), not the full [p2_chunks][Kp] block
+  const size_t part_rows =
+      g.variant == kSparse ? (size_t)sp_dense_rows(g) : (size_t)g.p2_chunks * g.Kp;
+  off = align256(off + sizeof(double) * part_rows * g.stat_w);
   L.aux = off;
   if (x32) {
     const size_t N = (size_t)g.N;
@@ -398,7 +413,8 @@ static int run_reduce(const Geom& g, const float* X, Ws& w, float* mu, float* va
     if (rc) return rc;
     return check_hip(launch_reduce_sparse(g, w.part, g.p2_chunks, nullptr, nullptr, 0, w.lnsum,
                                           mu, var, lp, params_next, bias_next, nullptr, s,
-                                          kReduceFlagged, w.x.flag),
+                                          kReduceFlagged, w.x.flag, nullptr, nullptr, nullptr,
+                                          nullptr, w.sp.nflag),
                      "reduction / M-step (exact components)");
   }
   if (g.variant != kX32)
@@ -441,8 +457,8 @@ static int run_pass2(const Geom& g, const float* X, Ws& w, hipStream_t s) {
     int rc = check_hip(launch_pass2_sparse(g, X, w.x, w.sp, w.ln2, s),
                        "pass 2 (sparse statistics)");
     if (rc) return rc;
-    return check_hip(launch_pass2_mfma_dyn(g, w.sp.Xo, w.params, w.bias, w.sp.ln2o, w.part,
-                                           w.sp.nov, s),
+    return check_hip(launch_pass2_mfma_dyn(g, X, w.params, w.bias, w.ln2, w.part, w.sp.nov,
+                                           w.sp.ovidx, s),
                      "pass 2 (overflow points)");
   }
   hipError_t e =
@@ -609,10 +625,12 @@ int fgmm_workspace_region(long N, int K, int d, int variant, const char* name,
 
 size_t fgmm_workspace_bytes(long N, int K, int d, int variant) {
   if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
+  // every entry point: some run the fp64 dense kernels for a small, sparse,
+  // mixed or x32 request (Pass 2 from a caller's log-normalizer, the
+  // gamma-returning E-steps), whose layout can be the larger one
   const size_t own = make_layout(make_geom(N, K, d, variant)).total;
-  if (resolve_variant(N, K, d, variant) != kSmall) return own;
-  // the stage entry points run the dense kernels for a small problem
-  const size_t dense = make_layout(make_geom(N, K, d, estep_variant(K, d, kSmall))).total;
+  const int r = resolve_variant(N, K, d, variant);
+  const size_t dense = make_layout(make_geom(N, K, d, estep_variant(K, d, r))).total;
   return own > dense ? own : dense;
 }
 

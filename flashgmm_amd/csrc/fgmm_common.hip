@@ -242,7 +242,8 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               const int* __restrict__ ndyn, long chunk2,
                               const int* __restrict__ pstart, const float* __restrict__ dmass,
                               int nblk, const double* __restrict__ glob,
-                              int* __restrict__ kmap, int* __restrict__ nflag) {
+                              int* __restrict__ kmap, int* __restrict__ nflag, int ov_cap,
+                              int rows_fl) {
   __shared__ double red[16];
   __shared__ double redn[5 * 16];   // five block sums at once (up to 16 wavefronts)
   __shared__ double nk_sh;
@@ -271,8 +272,13 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   const size_t row = (size_t)stat_w;
   const size_t kstride = (size_t)Kp * row;
   // sparse variant: partial rows of the dense pass over the overflow points
+  // (their chunking follows the device count, as the pass laid them out)
   int S2 = 0;
-  if (part2 != nullptr) S2 = (int)(((long)*ndyn + chunk2 - 1) / chunk2);
+  if (part2 != nullptr) {
+    const long nd = *ndyn;
+    const long c2 = sp_ov_chunk(nd, chunk2, ov_cap);
+    S2 = (int)((nd + c2 - 1) / c2);
+  }
   // rows of component k: part[s][k] for s < S, or (sparse, pstart) the
   // contiguous piece rows pstart[k] .. pstart[k+1]
   const double* pb = part + (size_t)k * row;
@@ -285,6 +291,15 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     Sk = (np + G - 1) / G;
     pb = part + (size_t)r0 * row;
     kst = row * G;
+  }
+  if (stage == kReduceFlagged && nflag != nullptr) {
+    // sparse: the flagged pass's rows of compact slot flag[k] - 1
+    const int kact = (*nflag + 15) & ~15;
+    int nc = 1;
+    sp_fl_chunk(N, S, rows_fl, kact, &nc);
+    Sk = nc;
+    pb = part + (size_t)(flag[k] - 1) * row;
+    kst = (size_t)kact * row;
   }
   {
     // n_k: chunk partials split across the block, merged in a fixed order
@@ -401,10 +416,16 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   if (stage == kReduceFlagging) {
     const bool bad = bad_sh != 0;
     if (threadIdx.x == 0) {
-      flag[k] = bad ? 1 : 0;
       // sparse: the flagged components' list for the exact pass (slot order
-      // is free: a component's sums do not depend on its slot)
-      if (bad && kmap != nullptr) kmap[atomicAdd(nflag, 1)] = k;
+      // is free: a component's sums do not depend on its slot); flag holds
+      // the slot + 1, where stage 2 finds the component's rows
+      if (bad && kmap != nullptr) {
+        const int slot = atomicAdd(nflag, 1);
+        kmap[slot] = k;
+        flag[k] = slot + 1;
+      } else {
+        flag[k] = bad ? 1 : 0;
+      }
     }
     if (bad) return;   // statistics recomputed exactly, then reduced in stage 2
   }
@@ -453,7 +474,7 @@ hipError_t launch_reduce(const Geom& g, const double* part, const double* lnsum,
                      g.Kp, g.d, g.dp, g.p2_chunks, g.stat_w, part, lnsum, g.p1_blocks,
                      n_k, s_k, sq_k, new_mu, new_var, new_log_pi, params_next,
                      bias_next, ll_out, standard, stage, flag, nullptr, nullptr, 1L, nullptr,
-                     nullptr, 0, nullptr, nullptr, nullptr);
+                     nullptr, 0, nullptr, nullptr, nullptr, 1, 0);
   return hipGetLastError();
 }
 
@@ -466,14 +487,15 @@ hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const 
   if (g.variant != kSparse || stage == kReduceAll || flag == nullptr || S < 1 ||
       g.stat_w < 2 * g.dp + 4 || (part2 != nullptr && (ndyn == nullptr || chunk2 < 1)) ||
       (pstart != nullptr && (dmass == nullptr || glob == nullptr)) ||
-      ((kmap == nullptr) != (nflag == nullptr)) || (kmap != nullptr && stage != kReduceFlagging))
+      (kmap != nullptr && nflag == nullptr) || (kmap != nullptr && stage != kReduceFlagging) ||
+      (stage == kReduceFlagged && nflag == nullptr) || g.sp_ov_cap < 1 || g.sp_rows_fl < 16)
     return hipErrorInvalidValue;
   const int blocks = (params_next != nullptr || stage == kReduceFlagging) ? g.Kp : g.K;
   hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(kReduceThreadsMax), 0, s, g.variant, g.N,
                      g.K, g.Kp, g.d, g.dp, S, g.stat_w, part, lnsum, g.p1_blocks, nullptr,
                      nullptr, nullptr, new_mu, new_var, new_log_pi, params_next, bias_next,
                      ll_out, 0, stage, flag, part2, ndyn, chunk2 < 1 ? 1L : chunk2, pstart,
-                     dmass, g.p1_blocks, glob, kmap, nflag);
+                     dmass, g.p1_blocks, glob, kmap, nflag, g.sp_ov_cap, g.sp_rows_fl);
   return hipGetLastError();
 }
 

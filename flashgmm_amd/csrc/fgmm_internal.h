@@ -72,6 +72,9 @@ struct Geom {
   int sp_C;         // list entries per point (more: the point takes the dense path)
   long sp_chunk;    // points per sort chunk
   int sp_nchunk;
+  // sparse: the dense fp64 passes' partial rows (see sp_dense_rows)
+  int sp_rows_fl;   // rows of the flagged-component pass: chunk x compact slot
+  int sp_ov_cap;    // point chunks of the overflow-point pass (rows: x Kp)
 };
 
 // Byte offsets of the workspace regions (all 256-byte aligned).
@@ -123,7 +126,7 @@ constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
 // component) at most.
 constexpr double kSpFloor = 0x1p-126;
 constexpr int kSpBound = 0x40000000;
-constexpr int kSpCap = 32;            // list entries per point (at most K)
+constexpr int kSpCap = 16;            // list entries per point (at most K)
 constexpr int kSpPts = 256;           // points per sort chunk
 constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
 constexpr int kSpPiece = 64;          // entries per accumulation piece (at least)
@@ -149,14 +152,37 @@ struct SpWs {
   double* glob;        // [4] N 2^-126 (with margin), max_n max_j |x_nj|, its square
   int2* sorted;        // [N * C] (point, float gamma bits) by (component, point)
   double* prow;        // [npiece_cap][stat_w] piece sums
-  float* Xo;           // [N][d] rows of the overflow points
-  double* ln2o;        // [N] their log-normalizers
+  int* ovidx;          // [N] the overflow points' indices, in point order
   int* kmap;           // [Kp] flagged components, any order (-1 = padding)
   int* nflag;          // [1]
 };
 // Piece rows: a fixed budget; the device widens the pieces past kSpPiece
 // entries when the lists hold more than kSpPiece x budget entries.
 inline long sp_piece_budget(const Geom& g) { return g.N / 64 > 4096 ? g.N / 64 : 4096; }
+// Dense fp64 passes of the sparse variant, sized from device counts rather
+// than worst cases.  Flagged components: their rows are indexed by compact
+// slot, (chunk c, slot i) at c * kact + i with kact = round_up(nflag, 16),
+// over nchunks = min(p2_chunks, max(1, sp_rows_fl / kact)) point chunks of
+// round_up(ceil(N / nchunks), 64) points; overflow points: at most sp_ov_cap
+// chunks of max(p2_chunk, round_up(ceil(n_ov / sp_ov_cap), 64)) points, rows
+// (c, k) at c * Kp + k.  Both keep chunks <= 16384 points (the bound of the
+// fp32 sum of gamma x) and share the `part` region.
+__host__ __device__ inline long sp_fl_chunk(long N, int p2_chunks, int rows_fl, int kact,
+                                            int* nchunks) {
+  int nc = kact > 0 ? rows_fl / kact : p2_chunks;
+  nc = nc < 1 ? 1 : (nc > p2_chunks ? p2_chunks : nc);
+  const long chunk = ((N + nc - 1) / nc + 63) / 64 * 64;
+  *nchunks = (int)((N + chunk - 1) / chunk);
+  return chunk;
+}
+__host__ __device__ inline long sp_ov_chunk(long n_ov, long base_chunk, int ov_cap) {
+  const long c = ((n_ov + ov_cap - 1) / ov_cap + 63) / 64 * 64;
+  return c > base_chunk ? c : base_chunk;
+}
+inline long sp_dense_rows(const Geom& g) {
+  const long ov = (long)g.sp_ov_cap * g.Kp;
+  return ov > g.sp_rows_fl ? ov : g.sp_rows_fl;
+}
 inline long sp_npiece_cap(const Geom& g) { return sp_piece_budget(g) + g.Kp + 1; }
 
 // Error model of the fp32 expanded distance (x32 variant).  ll32 is
@@ -269,15 +295,15 @@ hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const 
 // clears the flagged-component list (sp.kmap = -1, sp.nflag = 0).
 hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, const SpWs& sp,
                                const double* ln2, hipStream_t s);
-// fp64 matrix-core Pass 2 over the first *ndyn rows of X (device count, at
-// most g.N); chunks past them exit without writing.
+// fp64 matrix-core Pass 2 over the *ndyn points X[rowidx[i]] (device count,
+// at most g.N), in sp_ov_chunk chunks (at most g.sp_ov_cap); rows (c, k).
 hipError_t launch_pass2_mfma_dyn(const Geom& g, const float* X, const double* P,
                                  const double* bias, const double* ln2, double* part,
-                                 const int* ndyn, hipStream_t s);
+                                 const int* ndyn, const int* rowidx, hipStream_t s);
 // fp64 matrix-core Pass 2 over all points for the listed components kmap[i],
 // i < *kdyn (-1 beyond, up to a multiple of 16), their coefficients gathered
-// from the fragment-ordered P / bias; the row of listed component i is
-// part[s][kmap[i]].
+// from the fragment-ordered P / bias; the rows are (chunk, slot i) as
+// sp_fl_chunk lays them out.
 hipError_t launch_pass2_mfma_map(const Geom& g, const float* X, const double* P,
                                  const double* bias, const double* ln2, double* part,
                                  const int* kmap, const int* kdyn, hipStream_t s);

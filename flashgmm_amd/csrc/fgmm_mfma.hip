@@ -229,7 +229,8 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const double* __restrict__ P,
     const double* __restrict__ bias, const double* __restrict__ ln2,
     double* __restrict__ part, long chunk, int nchunks, int kblocks, int stat_w,
-    const int* __restrict__ ndyn, const int* __restrict__ kmap, const int* __restrict__ kdyn) {
+    const int* __restrict__ ndyn, const int* __restrict__ kmap, const int* __restrict__ kdyn,
+    const int* __restrict__ rowidx, int rows_fl) {
   constexpr int Q = DP / 4, S1 = DP / 2;
   constexpr int XS = DP + 20;  // LDS row stride in floats (16-byte aligned rows)
   constexpr int NFT = DP / 16;
@@ -241,9 +242,13 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
   // (ndyn: rows, kdyn: compacted components) only the blocks and chunks that
   // hold work are enumerated and the grid strides over them; otherwise the
   // grid has one workgroup per item.
+  // (ndyn: the rows are X[rowidx[i]], i < *ndyn, in sp_ov_chunk chunks of
+  // which `nchunks` is the cap; kdyn with rows_fl: rows by compact slot in
+  // sp_fl_chunk chunks of which `nchunks` is the cap)
   if (ndyn != nullptr) {
     const long nd = *ndyn;
     N = nd < N ? nd : N;
+    chunk = sp_ov_chunk(N, chunk, nchunks);
     nchunks = (int)((N + chunk - 1) / chunk);
   }
   int kact = Kp;   // compacted components: the first round_up(*kdyn, 16) slots
@@ -251,6 +256,7 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
     kact = (*kdyn + 15) & ~15;
     const int per = (SPLIT ? 1 : kP2Waves) * 16;
     kblocks = (kact + per - 1) / per;
+    if (rows_fl > 0) chunk = sp_fl_chunk(N, nchunks, rows_fl, kact, &nchunks);
   }
   const int nitems = kblocks * ((nchunks + 7) / 8 * 8);
   auto body = [&](const int item) {   // one item; its returns end the item
@@ -305,7 +311,8 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
       const long nn = t0 + row;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (nn < p1) {
-        const float* src = X + (size_t)nn * d + j;
+        const long ri = rowidx != nullptr ? (long)rowidx[nn] : nn;
+        const float* src = X + (size_t)ri * d + j;
         if (VEC) {
           if (j < d) v = *reinterpret_cast<const float4*>(src);
         } else {
@@ -317,7 +324,10 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
       }
       pre[i] = v;
     }
-    if (tid < kP2Tile) preL = (t0 + tid < p1) ? ln2[t0 + tid] : INFINITY;  // gamma = 0 past the chunk
+    if (tid < kP2Tile) {   // gamma = 0 past the chunk
+      const long nn = t0 + tid;
+      preL = nn < p1 ? ln2[rowidx != nullptr ? (long)rowidx[nn] : nn] : INFINITY;
+    }
   };
   auto lstore = [&](int buf) {
 #pragma unroll
@@ -454,8 +464,12 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
   // partial row of local component R (kmap: the compacted slot's component,
   // -1 for padding)
   auto row = [&](int R) -> double* {
-    const int kr = kmap != nullptr ? kmap[ks * 16 + R] : ks * 16 + R;
-    return kr < 0 ? nullptr : part + ((size_t)chunk_id * Kp + (size_t)kr) * stat_w;
+    const int slot = ks * 16 + R;
+    const int kr = kmap != nullptr ? kmap[slot] : slot;
+    if (kr < 0) return nullptr;
+    if (kmap != nullptr && rows_fl > 0)   // compact: (chunk, slot)
+      return part + ((size_t)chunk_id * kact + (size_t)slot) * stat_w;
+    return part + ((size_t)chunk_id * Kp + (size_t)kr) * stat_w;
   };
   // fp32 16x16x4 accumulator: register r of lane (g, c) is row 4g+r;
   // fp64 16x16x4 accumulator: register r of lane (g, c) is row 4r+g.
@@ -523,7 +537,8 @@ template <int DP, bool VEC>
 static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
                             const double* bias, const double* ln2, double* part,
                             hipStream_t s, const int* ndyn = nullptr,
-                            const int* kmap = nullptr, const int* kdyn = nullptr) {
+                            const int* kmap = nullptr, const int* kdyn = nullptr,
+                            const int* rowidx = nullptr) {
   const int padded = (g.p2_chunks + 7) / 8 * 8;
   // device-counted work: a grid of at most kPersist workgroups strides over it
   // (kPersistRows for the overflow points, usually none: an empty launch of
@@ -533,20 +548,21 @@ static hipError_t p2_launch(const Geom& g, const float* X, const double* P,
     const int items = g.Kp / 16 * padded;
     hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, true, true>), dim3(items < kPersist ? items : kPersist),
                        dim3(64 * kP2Waves), 0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part,
-                       g.p2_chunk, g.p2_chunks, g.Kp / 16, g.stat_w, ndyn, kmap, kdyn);
+                       g.p2_chunk, g.p2_chunks, g.Kp / 16, g.stat_w, ndyn, kmap, kdyn, nullptr,
+                       g.sp_rows_fl);
     return hipGetLastError();
   }
   const int items = g.p2_kblocks * padded;
   if (ndyn != nullptr) {
     hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false, true>),
                        dim3(items < kPersistRows ? items : kPersistRows), dim3(64 * kP2Waves), 0, s, X,
-                       g.N, g.d, g.Kp, P, bias, ln2, part, g.p2_chunk, g.p2_chunks,
-                       g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
+                       g.N, g.d, g.Kp, P, bias, ln2, part, g.p2_chunk, g.sp_ov_cap,
+                       g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn, rowidx, 0);
     return hipGetLastError();
   }
   hipLaunchKernelGGL((pass2_mfma_kernel<DP, VEC, false, false>), dim3(items), dim3(64 * kP2Waves),
                      0, s, X, g.N, g.d, g.Kp, P, bias, ln2, part, g.p2_chunk, g.p2_chunks,
-                     g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn);
+                     g.p2_kblocks, g.stat_w, ndyn, kmap, kdyn, nullptr, 0);
   return hipGetLastError();
 }
 
@@ -595,14 +611,14 @@ hipError_t launch_pass2_mfma(const Geom& g, const float* X, const double* P,
 
 hipError_t launch_pass2_mfma_dyn(const Geom& g, const float* X, const double* P,
                                  const double* bias, const double* ln2, double* part,
-                                 const int* ndyn, hipStream_t s) {
-  if (ndyn == nullptr) return hipErrorInvalidValue;
+                                 const int* ndyn, const int* rowidx, hipStream_t s) {
+  if (ndyn == nullptr || g.sp_ov_cap < 1) return hipErrorInvalidValue;
   const bool v = x_is_vec(X, g.d);
   switch (g.dp) {
 #define FGMM_P2(D)                                                       \
   case D:                                                               \
-    return v ? p2_launch<D, true>(g, X, P, bias, ln2, part, s, ndyn)           \
-             : p2_launch<D, false>(g, X, P, bias, ln2, part, s, ndyn);
+    return v ? p2_launch<D, true>(g, X, P, bias, ln2, part, s, ndyn, nullptr, nullptr, rowidx) \
+             : p2_launch<D, false>(g, X, P, bias, ln2, part, s, ndyn, nullptr, nullptr, rowidx);
     FGMM_P2(16) FGMM_P2(32) FGMM_P2(48) FGMM_P2(64) FGMM_P2(80) FGMM_P2(96)
     FGMM_P2(112) FGMM_P2(128)
 #undef FGMM_P2
@@ -614,7 +630,7 @@ hipError_t launch_pass2_mfma_dyn(const Geom& g, const float* X, const double* P,
 hipError_t launch_pass2_mfma_map(const Geom& g, const float* X, const double* P,
                                  const double* bias, const double* ln2, double* part,
                                  const int* kmap, const int* kdyn, hipStream_t s) {
-  if (kmap == nullptr || kdyn == nullptr) return hipErrorInvalidValue;
+  if (kmap == nullptr || kdyn == nullptr || g.sp_rows_fl < 16) return hipErrorInvalidValue;
   const bool v = x_is_vec(X, g.d);
   switch (g.dp) {
 #define FGMM_P2(D)                                                       \

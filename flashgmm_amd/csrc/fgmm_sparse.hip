@@ -367,8 +367,7 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
     const int* __restrict__ ecnt, const int* __restrict__ fcap, const int* __restrict__ seg,
     const int* __restrict__ off,
     const int* __restrict__ ooff, const int* __restrict__ pcnt, const float* __restrict__ X,
-    const double* __restrict__ ln2, int2* __restrict__ sorted, float* __restrict__ Xo,
-    double* __restrict__ ln2o) {
+    const double* __restrict__ ln2, int2* __restrict__ sorted, int* __restrict__ ovidx) {
   extern __shared__ int rs[];   // [Kp] first index of each component in the chunk
   __shared__ int sh[kT];
   __shared__ int ovn[kSpPts];   // overflow points of the chunk, in order
@@ -400,12 +399,7 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
   const int nv = nov_sh;
   if (nv == 0) return;
   const long base = ooff[ch];
-  for (long idx = tid; idx < (long)nv * d; idx += kT) {
-    const int rr = (int)(idx / d), j = (int)(idx - (long)rr * d);
-    const long n = p0 + ovn[rr];
-    Xo[(size_t)(base + rr) * d + j] = X[(size_t)n * d + j];
-    if (j == 0) ln2o[base + rr] = ln2[n];
-  }
+  for (int rr = tid; rr < nv; rr += kT) ovidx[base + rr] = (int)(p0 + ovn[rr]);
 }
 
 // ---------------------------------------------------------------------------
@@ -596,7 +590,7 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(sp_place_kernel, dim3(g.sp_nchunk), dim3(kT), sizeof(int) * (size_t)g.Kp,
                      s, g.N, g.d, g.Kp, g.sp_C, g.sp_nchunk, sp.blk, sp.ecnt, sp.fcap, sp.seg,
-                     sp.cnt, sp.ocnt, w.pcnt, X, ln2, sp.sorted, sp.Xo, sp.ln2o);
+                     sp.cnt, sp.ocnt, w.pcnt, X, ln2, sp.sorted, sp.ovidx);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (g.dp <= 16) e = piece_launch<4>(g, X, sp, s);
   else if (g.dp <= 32) e = piece_launch<8>(g, X, sp, s);

@@ -80,7 +80,7 @@ int fgmm_error_model(int d, double* c_x32, double* c_bf16);
  * Diagnostic view of the sparse variant's workspace (host-only query): byte
  * offset and size of a named region that holds, after a call, counts of the
  * last iteration -- "pcnt" (int [N]: list entries of each point, more than
- * min(K, 32) = the point took the dense path), "rowtot" (int [Kp]: listed
+ * min(K, 16) = the point took the dense path), "rowtot" (int [Kp]: listed
  * entries per component), "nov" (int [3]: overflow points, accumulation
  * pieces, entries per piece), "nflag" (int: components recomputed exactly).
  * FGMM_EINVAL for other variants or names.  No counterpart in the reference.

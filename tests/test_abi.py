@@ -53,7 +53,7 @@ def test_version_and_variant_table(lib):
     assert lib.fgmm_resolve_variant(262144, 128, 64, 0) == 5
     assert lib.fgmm_resolve_variant(4096, 64, 32, 0) == 2
     assert lib.fgmm_resolve_variant(65536, 9000, 64, 0) == 4        # K > 8192: mixed
-    assert lib.fgmm_resolve_variant(1 << 27, 256, 64, 0) == 4       # N * 32 >= 2^31
+    assert lib.fgmm_resolve_variant(1 << 27, 256, 64, 0) == 4       # N * 16 >= 2^31
     assert lib.fgmm_resolve_variant(4096, 8, 32, 0) == 6          # small: one launch
     assert lib.fgmm_resolve_variant(4096, 7, 32, 0) == 6
     assert lib.fgmm_resolve_variant(65536, 8, 32, 0) == 2         # too many workgroups

@@ -458,7 +458,7 @@ def test_x32_crowded_window_overflows_slots(cuda):
 
 def test_sparse_partial_overflow_and_repeatability(cuda):
     """40 nearly identical components around the origin and 8 separated ones:
-    points near the origin list ~40 pairs, more than the 32 entries a point
+    points near the origin list ~40 pairs, more than the 16 entries a point
     may list, and take the dense fp64 pass; the others take the listed pairs.
     Both kinds of rows meet in the reduction.  Two calls agree bit for bit."""
     import torch
@@ -535,3 +535,48 @@ def test_small_variant_extremes(cuda, N, K, d):
     _, _, _, traj = C.em_fit(*t, 3, variant="small")
     e = np.abs(traj.cpu().numpy() - traj_ref) / np.abs(traj_ref)
     assert e.max() <= 1e-4, e.max()
+
+
+def test_sparse_chunk_capacity_cut(cuda):
+    """12 nearly identical components near the origin and 4 far ones: a point
+    near the origin lists 12 exact pairs (within the 16 a point may list), so
+    a 256-point sort chunk holds ~2300 entries, more than the 2048 it may
+    keep; the points past the cut take the dense fp64 pass.  The workspace's
+    overflow count proves the cut happened (no list exceeds 16).  Against the
+    fp64 oracle, and two calls agree bit for bit."""
+    import ctypes
+    import torch
+    from flashgmm_amd import _lib
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(21)
+    N, d, near = 8192, 32, 6000
+    far = rng.uniform(-30, 30, (4, d))
+    Xa = rng.normal(0, 1, (near, d))
+    Xb = far[rng.integers(0, 4, N - near)] + rng.normal(0, 1, (N - near, d))
+    X = np.concatenate([Xa, Xb])[rng.permutation(N)].astype(np.float32)
+    mu = np.concatenate([rng.normal(0, 0.02, (12, d)), far]).astype(np.float32)
+    K = mu.shape[0]
+    var = rng.uniform(0.9, 1.1, (K, d)).astype(np.float32)
+    lp = np.full(K, -np.log(K), np.float32)
+    ref = O.c_em_fused(X, mu, var, lp)
+    t = to_dev(cuda, X, mu, var, lp)
+    print("[case] sparse chunk capacity cut", flush=True)
+    a = C.flash_em_fused(*t, variant="sparse")
+    torch.cuda.synchronize()
+    lib = _lib.load()
+    wsb = lib.fgmm_workspace_bytes(N, K, d, 5)
+    ws = _lib.workspace(cuda, wsb)
+    counts = {}
+    for name in ("pcnt", "nov"):
+        off, nb = ctypes.c_size_t(), ctypes.c_size_t()
+        _lib.check(lib.fgmm_workspace_region(N, K, d, 5, name.encode(), ctypes.byref(off),
+                                             ctypes.byref(nb)))
+        counts[name] = ws[off.value:off.value + nb.value].view(torch.int32).cpu().numpy()
+    assert counts["pcnt"].max() <= 16, counts["pcnt"].max()
+    assert counts["nov"][0] > 0, "no point was cut by the chunk capacity"
+    out = [o.cpu().numpy() for o in a]
+    check_ln(out[3], ref[3], "chunk cut")
+    check_params(out[:3], ref[:3], "chunk cut")
+    b = C.flash_em_fused(*t, variant="sparse")
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
