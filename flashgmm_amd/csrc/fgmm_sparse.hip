@@ -418,25 +418,39 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
   const int j = tid % L, h = tid / L;
   const int j0 = 4 * j;
   const int npiece = nov[1];
-  // the piece's entry range, loaded one piece ahead (grid <= capacity: the
-  // first load is in bounds, and unused past npiece)
-  int4 cur = pinfo[blockIdx.x];
-  for (int pc = blockIdx.x; pc < npiece; pc += gridDim.x) {
-    const int pn = pc + (int)gridDim.x;
-    const int4 nxp = pn < npiece ? pinfo[pn] : make_int4(0, 0, 0, 0);
+  constexpr int kStep = H * kAccUnroll;
+  const int G = (int)gridDim.x;
+  // Pieces are pipelined: the entry ranges are loaded two pieces ahead and
+  // the next piece's first batch of entries while this piece is summed.
+  // pinfo rows past npiece are not written: an absent piece reads row 0
+  // (always inside the capacity) and takes the empty range (0, 0) instead,
+  // a select of values, so the load stays a global load.  Weight 0 past a
+  // piece has no effect.
+  auto piece_at = [&](int i) {
+    const int4 v = pinfo[i < npiece ? i : 0];
+    return i < npiece ? v : make_int4(0, 0, 0, 0);
+  };
+  int4 cur = piece_at(blockIdx.x);
+  int4 nxt = piece_at(blockIdx.x + G);
+  int2 en[kAccUnroll];
+#pragma unroll
+  for (int u = 0; u < kAccUnroll; u++) {
+    const int eu = cur.x + h + u * H;
+    en[u] = eu < cur.y ? sorted[eu] : make_int2(0, 0);
+  }
+  for (int pc = blockIdx.x; pc < npiece; pc += G) {
     const int e0 = cur.x, e1 = cur.y;
-    cur = nxp;
-    double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
-    double nk = 0.0, eb = 0.0, es = 0.0, eq = 0.0;
-    // entries of the next batch are loaded while this batch's rows of X are
-    // in flight (weight 0 past the piece: no effect)
-    constexpr int kStep = H * kAccUnroll;
-    int2 en[kAccUnroll];
+    const int4 after = piece_at(pc + 2 * G);
+    int2 enx[kAccUnroll];   // the next piece's first batch
 #pragma unroll
     for (int u = 0; u < kAccUnroll; u++) {
-      const int eu = e0 + h + u * H;
-      en[u] = eu < e1 ? sorted[eu] : make_int2(0, 0);
+      const int eu = nxt.x + h + u * H;
+      enx[u] = eu < nxt.y ? sorted[eu] : make_int2(0, 0);
     }
+    double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
+    double nk = 0.0, eb = 0.0, es = 0.0, eq = 0.0;
+    // within a piece, the entries of the next batch are loaded while this
+    // batch's rows of X are in flight
     for (int e = e0 + h; e < e1; e += kStep) {
       int2 nx[kAccUnroll];
 #pragma unroll
@@ -513,6 +527,10 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
       row[2 * dp + tid] = t;
     }
     __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kAccUnroll; u++) en[u] = enx[u];
+    cur = nxt;
+    nxt = after;
   }
 }
 
