@@ -305,19 +305,36 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     // n_k: chunk partials split across the block, merged in a fixed order
     double t = 0.0;
     const double* p = pb + 2 * dp;
-    for (int s = threadIdx.x; s < Sk; s += blockDim.x) t += p[(size_t)s * kst];
-    if (S2 > 0) {
-      const double* p2 = part2 + (size_t)k * row + 2 * dp;
-      for (int s = threadIdx.x; s < S2; s += blockDim.x) t += p2[(size_t)s * kstride];
-    }
     if (stage == kReduceFlagging) {
       // n_k, the three error columns and (sparse) the never-pending bounds,
-      // reduced together
-      double v5[5] = {t, 0.0, 0.0, 0.0, 0.0};
-      for (int c = 1; c <= 3; c++)
-        for (int s = threadIdx.x; s < Sk; s += blockDim.x) v5[c] += p[(size_t)s * kst + c];
-      if (dmass != nullptr)
-        for (int b = threadIdx.x; b < nblk; b += blockDim.x) v5[4] += (double)dmass[(size_t)k * nblk + b];
+      // reduced together; a row's four columns are read at once, and the
+      // overflow rows and bounds requested before they are added
+      double v5[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+      for (int s = threadIdx.x; s < Sk; s += blockDim.x) {
+        const double* q = p + (size_t)s * kst;
+        const double a0 = q[0], a1 = q[1], a2 = q[2], a3 = q[3];
+        v5[0] += a0;
+        v5[1] += a1;
+        v5[2] += a2;
+        v5[3] += a3;
+      }
+      if (S2 > 0) {
+        const double* p2 = part2 + (size_t)k * row + 2 * dp;
+        for (int s = threadIdx.x; s < S2; s += blockDim.x) v5[0] += p2[(size_t)s * kstride];
+      }
+      if (dmass != nullptr) {
+        const float* dm = dmass + (size_t)k * nblk;
+        int b = threadIdx.x;
+        for (; b + 3 * (int)blockDim.x < nblk; b += 4 * blockDim.x) {
+          const float f0 = dm[b], f1 = dm[b + blockDim.x], f2 = dm[b + 2 * blockDim.x],
+                      f3 = dm[b + 3 * blockDim.x];
+          v5[4] += (double)f0;
+          v5[4] += (double)f1;
+          v5[4] += (double)f2;
+          v5[4] += (double)f3;
+        }
+        for (; b < nblk; b += blockDim.x) v5[4] += (double)dm[b];
+      }
       block_sum_f64_n<5>(v5, redn);
       t = v5[0];
       if (threadIdx.x == 0) {
@@ -334,6 +351,11 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
         }
       }
     } else {
+      for (int s = threadIdx.x; s < Sk; s += blockDim.x) t += p[(size_t)s * kst];
+      if (S2 > 0) {
+        const double* p2 = part2 + (size_t)k * row + 2 * dp;
+        for (int s = threadIdx.x; s < S2; s += blockDim.x) t += p2[(size_t)s * kstride];
+      }
       t = block_sum_f64(t, red);
     }
     if (threadIdx.x == 0) {

@@ -115,6 +115,7 @@ struct X32Ws {
   float* dmass;        // [Kp][p1_blocks] bound on the unlisted responsibility mass
 };
 constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
+constexpr int kX1Waves = 8;     // Pass-1 wavefronts per workgroup of the x32 family (16 points each)
 
 // Sparse variant.  Pass 1 lists every pair it evaluates exactly (those whose
 // fp32 upper bound reaches within 40 bits of the point's best lower bound);

@@ -250,17 +250,26 @@ __global__ __launch_bounds__(kT) void sp_rowscan_kernel(int Kp, int nchunk, int*
   if (k >= Kp) return;
   int* row = cnt + (size_t)k * nchunk;
   int carry = 0;
-  for (int b = 0; b < nchunk; b += 64) {
-    const int i = b + lane;
-    const int v = i < nchunk ? row[i] : 0;
-    int x = v;
+  constexpr int kB = 8;   // 64-chunk steps whose counts are loaded before they are scanned
+  for (int b0 = 0; b0 < nchunk; b0 += 64 * kB) {
+    int v[kB];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int u = __shfl_up(x, off, 64);
-      if (lane >= off) x += u;
+    for (int u = 0; u < kB; u++) {
+      const int i = b0 + 64 * u + lane;
+      v[u] = i < nchunk ? row[i] : 0;
     }
-    if (i < nchunk) row[i] = carry + x - v;
-    carry += __shfl(x, 63, 64);
+#pragma unroll
+    for (int u = 0; u < kB; u++) {
+      const int i = b0 + 64 * u + lane;
+      int x = v[u];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(x, off, 64);
+        if (lane >= off) x += t;
+      }
+      if (i < nchunk) row[i] = carry + x - v[u];
+      carry += __shfl(x, 63, 64);
+    }
   }
   if (lane == 0) rowtot[k] = carry;
 }
@@ -549,7 +558,15 @@ __global__ __launch_bounds__(kT) void sp_group_kernel(int d, int dp, int stat_w,
     for (int f = threadIdx.x; f < 2 * dp + 4; f += kT) {
       if ((f >= d && f < dp) || (f >= dp + d && f < 2 * dp)) continue;
       double a = out[f];
-      for (int q = 1; q < n; q++) a += out[(size_t)q * stat_w + f];
+      int q = 1;
+      for (; q + 8 <= n; q += 8) {   // eight rows in flight, summed in order
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = out[(size_t)(q + u) * stat_w + f];
+#pragma unroll
+        for (int u = 0; u < 8; u++) a += v[u];
+      }
+      for (; q < n; q++) a += out[(size_t)q * stat_w + f];
       out[f] = a;
     }
   }

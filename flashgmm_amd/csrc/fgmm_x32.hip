@@ -48,7 +48,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kW1 = 8;                  // Pass 1 wavefronts per workgroup
+constexpr int kW1 = kX1Waves;           // Pass 1 wavefronts per workgroup
 constexpr int kPts1 = 16 * kW1;         // Pass 1 points per workgroup
 constexpr int kThr1 = 64 * kW1;
 constexpr int kSub1 = 2;                // 16-component subtiles per LDS tile
@@ -158,7 +158,7 @@ __device__ inline void load_quarter32(const float* __restrict__ X, long n, long 
 // lanes' pending lists, entry i of thread t at i*512 + t (conflict-free).
 // ---------------------------------------------------------------------------
 template <int DP, bool VEC, int MODE>
-__global__ __launch_bounds__(512) void pass1_x32_kernel(
+__global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const float* __restrict__ P32,
     const float* __restrict__ bias32, const float* __restrict__ Z32,
     const double* __restrict__ V2, const double* __restrict__ b64,
