@@ -255,7 +255,7 @@ def run_gpu(cid, steps, warmup, variant):
     lp = torch.from_numpy(lp0).to(dev)
     lib = _lib.load()
     vname = C.resolve_variant(cfg.N, cfg.K, cfg.d, variant)
-    wsb = lib.fgmm_workspace_bytes(cfg.N, cfg.K, cfg.d, _lib.variant_code(variant))
+    wsb = lib.fgmm_em_fused_workspace_bytes(cfg.N, cfg.K, cfg.d, _lib.variant_code(variant))
 
     if warmup > 0:   # also builds the workspace
         C.em_fit(Xd, mu, var, lp, warmup, variant=variant)

@@ -123,13 +123,13 @@ Geom make_geom(long N, int K, int d, int variant) {
   g.sp_chunk = kSpPts;
   g.sp_nchunk = (int)((N + kSpPts - 1) / kSpPts);
   // dense fp64 passes of the sparse variant (sp_dense_rows): chunks of at
-  // most 16384 points; the flagged pass gets 8192 rows (about 512 work items
+  // most 16384 points; the flagged pass gets 4096 rows (about 256 work items
   // however many components are flagged), the overflow pass a quarter of
-  // |X| (at least 8 MiB) of rows
+  // |X| (at least 4 MiB) of rows
   const long min_chunks = (N + 16383) / 16384;
-  g.sp_rows_fl = (int)std::max<long>(8192, min_chunks * g.Kp);
+  g.sp_rows_fl = (int)std::max<long>(4096, min_chunks * g.Kp);
   const size_t row_set = sizeof(double) * (size_t)g.Kp * g.stat_w;
-  const size_t ov_bytes = std::max<size_t>(sizeof(float) * (size_t)N * d / 4, size_t(8) << 20);
+  const size_t ov_bytes = std::max<size_t>(sizeof(float) * (size_t)N * d / 4, size_t(4) << 20);
   g.sp_ov_cap = (int)std::min<long>(g.p2_chunks, std::max<long>(min_chunks, (long)(ov_bytes / row_set)));
   if (g.sp_ov_cap < 1) g.sp_ov_cap = 1;
   return g;
@@ -147,7 +147,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   };
   char* xm = take(sizeof(float) * N);
   char* pcnt = take(sizeof(int) * N);
-  char* pk = take(sizeof(int) * NC);
+  char* pk = take(sizeof(unsigned short) * NC);
   char* pv = take(sizeof(double) * NC);
   char* blk = take(sizeof(int2) * nch * kSpChunkCap);
   char* ecnt = take(sizeof(int) * nch);
@@ -161,7 +161,11 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
   char* pinfo = take(sizeof(int4) * npc);
   char* nov = take(sizeof(int) * 3);
   char* glob = take(sizeof(double) * 4);
-  char* sorted = take(sizeof(int2) * NC);
+  // the placed runs (point, gamma) reuse the lists' values: the chunk sort
+  // reads pv before the placement writes sorted, and the next Pass 1 writes
+  // pv after the piece sums have read sorted (one stream orders them)
+  static_assert(sizeof(int2) == sizeof(double), "sorted entries fill pv's slots");
+  char* sorted = pv;
   char* prow = take(sizeof(double) * npc * (size_t)g.stat_w);
   char* ovidx = take(sizeof(int) * N);
   char* kmap = take(sizeof(int) * Kp);
@@ -172,7 +176,7 @@ static size_t sparse_aux(const Geom& g, char* b, size_t off, X32Ws* x, SpWs* sp)
     x->dmass = reinterpret_cast<float*>(dmass);
     x->xm = reinterpret_cast<float*>(xm);
     x->pcnt = reinterpret_cast<int*>(pcnt);
-    x->pk = reinterpret_cast<int*>(pk);
+    x->pk = reinterpret_cast<unsigned short*>(pk);
     x->pv = reinterpret_cast<double*>(pv);
     x->pC = g.sp_C;
     x->flag = reinterpret_cast<int*>(flag);
@@ -633,6 +637,11 @@ size_t fgmm_workspace_bytes(long N, int K, int d, int variant) {
   const int r = resolve_variant(N, K, d, variant);
   const size_t dense = make_layout(make_geom(N, K, d, estep_variant(K, d, r))).total;
   return own > dense ? own : dense;
+}
+
+size_t fgmm_em_fused_workspace_bytes(long N, int K, int d, int variant) {
+  if (validate_shape(N, K, d, variant) != FGMM_OK) return 0;
+  return make_layout(make_geom(N, K, d, variant)).total;
 }
 
 int fgmm_em_fused(const float* X, const float* mu, const float* var, const float* log_pi,

@@ -108,7 +108,7 @@ struct X32Ws {
   float* cg;           // [N][kX32Slots] slot responsibilities (exact)
   int* flag;           // [Kp] components whose statistics are recomputed exactly
   // sparse variant: per-point pair lists written by Pass 1
-  int* pk;             // [N][pC] component (| kSpBound for a bound entry)
+  unsigned short* pk;  // [N][pC] component (| kSpBound for a bound entry)
   double* pv;          // [N][pC] exact ll2 (bound entry: upper bound of ll2)
   int* pcnt;           // [N] entries of the point (> pC: the list overflowed)
   int pC;
@@ -126,7 +126,8 @@ constexpr int kX1Waves = 8;     // Pass-1 wavefronts per workgroup of the x32 fa
 // Each remaining pair has gamma < 2^-126; one such pair per (point,
 // component) at most.
 constexpr double kSpFloor = 0x1p-126;
-constexpr int kSpBound = 0x40000000;
+constexpr int kSpBound = 0x8000;      // bound-entry flag of a list component (16-bit entries)
+static_assert(kSpBound > 8192, "the sparse variant's components (Kp <= 8192) fit below the flag");
 constexpr int kSpCap = 16;            // list entries per point (at most K)
 constexpr int kSpPts = 256;           // points per sort chunk
 constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
@@ -151,7 +152,8 @@ struct SpWs {
                        // (z >= 2 heads a group of z rows), component w
   int* nov;            // [3] overflow points, pieces, entries per piece
   double* glob;        // [4] N 2^-126 (with margin), max_n max_j |x_nj|, its square
-  int2* sorted;        // [N * C] (point, float gamma bits) by (component, point)
+  int2* sorted;        // [N * C] (point, float gamma bits) by (component, point);
+                       // shares the lists' pv memory (dead by then)
   double* prow;        // [npiece_cap][stat_w] piece sums
   int* ovidx;          // [N] the overflow points' indices, in point order
   int* kmap;           // [Kp] flagged components, any order (-1 = padding)

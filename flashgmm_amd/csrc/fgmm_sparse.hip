@@ -87,7 +87,8 @@ __device__ inline int block_excl_scan(int v, int* sh, int* total) {
 // per-chunk sort
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kT) void sp_sort_kernel(
-    long N, int Kp, int C, int nchunk, const int* __restrict__ pcnt, const int* __restrict__ pk,
+    long N, int Kp, int C, int nchunk, const int* __restrict__ pcnt,
+    const unsigned short* __restrict__ pk,
     const double* __restrict__ pv, const double* __restrict__ ln2, const float* __restrict__ xm,
     int2* __restrict__ blk, int* __restrict__ ecnt, int* __restrict__ fcap,
     int* __restrict__ cnt, int* __restrict__ ocnt, double* __restrict__ xsum) {
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     else m = c;
 #pragma unroll
     for (int i = 0; i < kPre; i++) {
-      kpre[i] = i < m ? pk[(size_t)n * C + i] : 0;
+      kpre[i] = i < m ? (int)pk[(size_t)n * C + i] : 0;
       vpre[i] = i < m ? pv[(size_t)n * C + i] : 0.0;
     }
   }
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     atomicMin(&cut_sh, tid);
     ov = 1;
   } else if (m > 0) {
-    const int* kr = pk + (size_t)n * C;
+    const unsigned short* kr = pk + (size_t)n * C;
     const double* vr = pv + (size_t)n * C;
     auto put = [&](int i, int kb, double v) {
       const int k = kb & (kSpBound - 1);

@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
     const double* __restrict__ V2, const double* __restrict__ b64,
     double* __restrict__ ln2, float* __restrict__ ln_out, double* __restrict__ lnsum,
     float* __restrict__ m32, float* __restrict__ xm, unsigned short* __restrict__ ck,
-    float* __restrict__ cg, int* __restrict__ pk, double* __restrict__ pv,
+    float* __restrict__ cg, unsigned short* __restrict__ pk, double* __restrict__ pv,
     int* __restrict__ pcnt, int pC, float* __restrict__ dmass) {
   constexpr bool SLOTS = MODE == kX1Slots, EMIT = MODE == kX1Emit;
   constexpr float kWinP1 = kWin;
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
         reinterpret_cast<double*>(plist)[a_] = v_;                                    \
         if (EMIT && pcp_ + e_ < pC) {                                                 \
           const size_t pb_ = (size_t)((long)blockIdx.x * kPts1 + wave * 16 + p_) * pC; \
-          pk[pb_ + pcp_ + e_] = k_;                                                   \
+          pk[pb_ + pcp_ + e_] = (unsigned short)k_;                                   \
           pv[pb_ + pcp_ + e_] = v_;                                                   \
         }                                                                             \
       }                                                                               \
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
           live_++;                                                                    \
         } else if (h_ >= th_ - kSpKeep) {                                             \
           if (bp_ < pC) {                                                             \
-            pk[pbase + bp_] = e_.x | kSpBound;                                        \
+            pk[pbase + bp_] = (unsigned short)(e_.x | kSpBound);                      \
             pv[pbase + bp_] = (double)h_;                                             \
           }                                                                           \
           bp_++;                                                                      \

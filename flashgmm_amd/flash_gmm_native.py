@@ -80,9 +80,12 @@ def _params(X, mu, var, log_pi, fn):
     return (X.contiguous(), *out, N, K, d)
 
 
-def _ws(X, N, K, d, variant):
+def _ws(X, N, K, d, variant, fused=False):
+    """The cached device workspace, grown to what the call needs: the fused
+    iteration and the device loop need less than the other entry points."""
     lib = _lib.load()
-    nbytes = lib.fgmm_workspace_bytes(N, K, d, variant)
+    nbytes = (lib.fgmm_em_fused_workspace_bytes if fused else lib.fgmm_workspace_bytes)(
+        N, K, d, variant)
     if nbytes == 0:   # the library rejected the shape; report its reason
         raise RuntimeError("flashgmm_amd: " + lib.fgmm_last_error().decode(errors="replace"))
     return _lib.workspace(X.device, nbytes), nbytes
@@ -107,7 +110,7 @@ def flash_em_fused(X, mu, var, log_pi, BN: int = 64, BK: int = 8, *, variant=Non
         return [new_mu, new_var, new_log_pi, ln]
     v = _lib.variant_code(variant)
     lib = _lib.load()
-    ws, nbytes = _ws(X, N, K, d, v)
+    ws, nbytes = _ws(X, N, K, d, v, fused=True)
     _lib.check(lib.fgmm_em_fused(_ptr(X), _ptr(mu), _ptr(var), _ptr(log_pi), N, K, d, v,
                                  _ptr(new_mu), _ptr(new_var), _ptr(new_log_pi), _ptr(ln),
                                  _ptr(ws), nbytes, _lib.stream_handle(X.device)))
@@ -306,7 +309,7 @@ def em_fit(X, mu0, var0, log_pi0, iters: int, *, variant=None):
         return mu, var, log_pi, traj
     v = _lib.variant_code(variant)
     lib = _lib.load()
-    ws, nbytes = _ws(X, N, K, d, v)
+    ws, nbytes = _ws(X, N, K, d, v, fused=True)
     _lib.check(lib.fgmm_em_fit(_ptr(X), _ptr(mu0), _ptr(var0), _ptr(log_pi0), N, K, d, iters, v,
                                _ptr(mu), _ptr(var), _ptr(log_pi), _ptr(traj), _ptr(ws), nbytes,
                                _lib.stream_handle(X.device)))

@@ -92,6 +92,15 @@ int fgmm_workspace_region(long N, int K, int d, int variant, const char* name,
 size_t fgmm_workspace_bytes(long N, int K, int d, int variant);
 
 /*
+ * Workspace bytes that fgmm_em_fused and fgmm_em_fit need (<=
+ * fgmm_workspace_bytes: the stage entry points and the gamma-returning
+ * E-steps can need more, since some run the dense kernels for a sparse
+ * request).  No counterpart in the reference, whose extension allocates
+ * its temporaries itself (flash_gmm/csrc/flash_gmm_cuda.cu:402-504).
+ */
+size_t fgmm_em_fused_workspace_bytes(long N, int K, int d, int variant);
+
+/*
  * One fused EM iteration: precompute -> Pass 1 (log-normalizer) -> Pass 2
  * (sufficient statistics) -> M-step.  Outputs new_mu[K][d], new_var[K][d],
  * new_log_pi[K] and log_normalizer[N] (= log p(x_n) under the INPUT
@@ -113,7 +122,7 @@ int fgmm_em_fused(const float* X, const float* mu, const float* var,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.
  * Its scratch is a static device array of the library,
  * fgmm_em_fused_noalloc_max_bytes() = 64 MiB on each GPU it runs on, held
- * until the process ends; problems whose fgmm_workspace_bytes exceed it are
+ * until the process ends; problems whose fgmm_em_fused_workspace_bytes exceed it are
  * rejected with FGMM_EWORKSPACE before any device work.  The call allocates
  * nothing (no hipMalloc / hipFree).  Results equal fgmm_em_fused's.  Every
  * call on one GPU shares that GPU's scratch: calls that overlap on one GPU

@@ -77,6 +77,23 @@ def test_workspace_bytes(lib):
     assert lib.fgmm_workspace_bytes(10, 8, 257, 0) == 0
 
 
+def test_fused_workspace_bytes(lib):
+    """The fused iteration's workspace is what it validates against, never
+    more than the all-entry-point figure, and within 2 x |X| for the sparse
+    default at C2, C4 and C5 (lists, sorted runs sharing the lists' values,
+    piece rows, dense-fallback rows sized from device counts)."""
+    for N, K, d in ((4096, 8, 32), (65536, 256, 128), (262144, 128, 64), (65536, 1024, 64),
+                    (1048576, 512, 128), (1, 1, 1), (5, 3, 256)):
+        for v in (0, 1, 2, 4, 5):
+            full = lib.fgmm_workspace_bytes(N, K, d, v)
+            b = lib.fgmm_em_fused_workspace_bytes(N, K, d, v)
+            assert (b == 0) == (full == 0)
+            assert b <= full and b % 256 == 0
+    for N, K, d in ((65536, 256, 128), (65536, 1024, 64), (1048576, 512, 128)):
+        assert lib.fgmm_em_fused_workspace_bytes(N, K, d, 0) <= 2 * 4 * N * d
+    assert lib.fgmm_em_fused_workspace_bytes(0, 8, 32, 0) == 0
+
+
 def test_estep_workspace_bytes(lib):
     for N, K, d in ((4096, 8, 32), (65536, 256, 128), (5, 3, 256), (1, 1, 1)):
         # the E-steps run the fp64 matrix-core (or vector) layout
