@@ -101,7 +101,7 @@ std::vector<Tensor> flash_em_fused(Tensor X, Tensor mu, Tensor var, Tensor log_p
                                 new_lp.data_ptr<float>(), ln.data_ptr<float>()));
     return {new_mu, new_var, new_lp, ln};
   }
-  const size_t wsb = fgmm_workspace_bytes(N, K, d, FGMM_VARIANT_AUTO);
+  const size_t wsb = fgmm_em_fused_workspace_bytes(N, K, d, FGMM_VARIANT_AUTO);
   auto ws = workspace(X, wsb);
   check_gpu(fgmm_em_fused(X.data_ptr<float>(), mu.data_ptr<float>(), var.data_ptr<float>(),
                           log_pi.data_ptr<float>(), N, K, d, FGMM_VARIANT_AUTO,
