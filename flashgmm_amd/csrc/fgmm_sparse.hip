@@ -49,7 +49,8 @@ constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
 constexpr int kAccUnroll = 4;      // entries per lane group in flight
-constexpr int kPre = 4;            // list entries per point requested ahead in the chunk sort
+constexpr int kPre = kSpCap;       // list entries per point requested ahead in the chunk sort:
+                                   // all of them, so a long list costs no extra round trips
 constexpr int kSpCountMax = 2048;  // up to this Kp the chunk sort is a counting sort
 constexpr int kPieceGrid = 2048;   // workgroups of the piece kernel (grid-stride)
 constexpr int kGroupGrid = 256;    // group fold: at least this many workgroups (grid-stride),
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     ek_sh = 0;
     ep_sh = 0;
   }
-  // one point per thread; its log-normalizer and first kPre entries are
-  // requested before the scan (i < m <= C: in bounds)
+  // one point per thread; its log-normalizer and its entries (at most
+  // C <= kPre) are requested before the scan (i < m <= C: in bounds)
   const long n = p0 + tid;
   int m = 0, ov = 0;
   double s1 = 0.0, l2 = 0.0;
@@ -137,8 +138,6 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     atomicMin(&cut_sh, tid);
     ov = 1;
   } else if (m > 0) {
-    const unsigned short* kr = pk + (size_t)n * C;
-    const double* vr = pv + (size_t)n * C;
     auto put = [&](int i, int kb, double v) {
       const int k = kb & (kSpBound - 1);
       float gam = exp2f((float)(v - l2));
@@ -155,7 +154,6 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
 #pragma unroll
     for (int i = 0; i < kPre; i++)
       if (i < m) put(i, kpre[i], vpre[i]);
-    for (int i = kPre; i < m; i++) put(i, kr[i], vr[i]);
     atomicMax(&ep_sh, pos + m);
   }
   atomicAdd(&ov_sh, ov);
@@ -593,7 +591,7 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
   if (g.variant != kSparse || g.dp > 128 || g.Kp > 8192 || g.stat_w < 2 * g.dp + 4 ||
       g.sp_chunk != kSpPts || (long)g.sp_nchunk * kSpPts < g.N || w.pk == nullptr ||
       w.pv == nullptr || w.pcnt == nullptr || w.dmass == nullptr || w.pC != g.sp_C ||
-      g.sp_C > kSpChunkCap)
+      g.sp_C > kPre)
     return hipErrorInvalidValue;
   // keys, gamma, histogram; the counting sort adds a point bitmask (32 B) and
   // a run start (4 B) per component
