@@ -56,7 +56,7 @@ sys.path.insert(0, ROOT)
 
 import numpy as np  # noqa: E402
 
-from flashgmm_amd.configs import CONFIGS, make_problem  # noqa: E402
+from flashgmm_amd.configs import CONFIGS, Config, make_problem, make_shape  # noqa: E402
 
 HBM_PEAK = 8.0e12        # B/s, MI355X
 FP32_PEAK = 157.3e12     # FLOP/s, MI355X dense fp32 (vector = matrix)
@@ -81,6 +81,12 @@ def parse():
                     help="instead of the resident benchmark, time the streaming iteration "
                          "(X in pinned host memory, chunks of this many rows copied while "
                          "the previous chunk computes) on --config")
+    ap.add_argument("--shape", default=None,
+                    help="N,K,d: instead of the five configurations, time this shape "
+                         "(configs.make_shape; one JSON line of its own)")
+    ap.add_argument("--overlap", action="store_true",
+                    help="with --shape: all components nearly identical (the sparse "
+                         "variant's worst case: every point takes the dense path)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before timing, run one plain device-to-device copy of this "
                          "many MiB (a known-size kernel to calibrate HBM byte counters)")
@@ -241,14 +247,13 @@ def sparse_counts(lib, cfg, variant, ws):
     return out
 
 
-def run_gpu(cid, steps, warmup, variant):
+def run_gpu(cfg, problem, steps, warmup, variant):
     import torch
     from flashgmm_amd import _lib
     from flashgmm_amd import flash_gmm_native as C
 
-    cfg = CONFIGS[cid]
     dev = torch.device("cuda:0")
-    X, mu0, var0, lp0 = make_problem(cid)
+    X, mu0, var0, lp0 = problem
     Xd = torch.from_numpy(X).to(dev)
     mu = torch.from_numpy(mu0).to(dev)
     var = torch.from_numpy(var0).to(dev)
@@ -265,6 +270,7 @@ def run_gpu(cid, steps, warmup, variant):
     _, _, _, traj = C.em_fit(Xd, mu, var, lp, steps, variant=variant)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    switched = int(lib.fgmm_em_fit_switch_iteration())
     counts = sparse_counts(lib, cfg, vname, _lib.workspace(dev, wsb))
     # profiled run: per-pass HIP events on the launch stream
     _lib.check(lib.fgmm_profile_enable(1))
@@ -285,7 +291,7 @@ def run_gpu(cid, steps, warmup, variant):
     del Xd, mu, var, lp
     return {"elapsed": elapsed, "elapsed_profiled": elapsed_prof, "kernels": kern,
             "ll_first": float(ll[0]), "ll_last": float(ll[-1]), "variant": vname,
-            "workspace_bytes": int(wsb), "counts": counts}
+            "workspace_bytes": int(wsb), "counts": counts, "dense_from_iteration": switched}
 
 
 def run_stream(cid, steps, warmup, chunk, variant):
@@ -384,7 +390,7 @@ def measure(cid, args, with_cpu):
     steps = cfg.iters if cid == 5 else args.steps
     print(f"[bench] C{cid}: N={cfg.N} K={cfg.K} d={cfg.d}, {steps} steps", file=sys.stderr,
           flush=True)
-    r = run_gpu(cid, steps, args.warmup, args.variant)
+    r = run_gpu(cfg, make_problem(cid), steps, args.warmup, args.variant)
     sec = r["elapsed"]
     ms_step = sec * 1e3 / steps
     roof = dominant_roofline(cfg, r["variant"], r["kernels"])
@@ -406,6 +412,7 @@ def measure(cid, args, with_cpu):
                     "between launches); value comes from the clean run",
         },
         "workspace_bytes": r["workspace_bytes"],
+        "dense_from_iteration": r["dense_from_iteration"],
         "x_bytes": cfg.N * cfg.d * 4,
         "ll_first": r["ll_first"], "ll_last": r["ll_last"],
     }
@@ -413,6 +420,33 @@ def measure(cid, args, with_cpu):
         out["cpu_baseline"] = cpu_baseline(cid, args.cpu_seconds)
         out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     return out
+
+
+def measure_shape(args):
+    """--shape N,K,d [--overlap]: the device loop on configs.make_shape's
+    problem, timed as the configurations are (clean run for the value,
+    profiled run for the per-pass durations); no CPU baseline."""
+    N, K, d = (int(v) for v in args.shape.split(","))
+    cfg = Config(0, N, K, d, -5.0, 5.0, "uniform", 0.5, 1.5, None, 0.0, args.steps,
+                 "overlapping components" if args.overlap else "custom shape")
+    r = run_gpu(cfg, make_shape(N, K, d, args.overlap), args.steps, args.warmup, args.variant)
+    ms_step = r["elapsed"] * 1e3 / args.steps
+    return {
+        "metric": f"EM iters/s (N={N},K={K},d={d} fp32{', overlapping components' if args.overlap else ''})",
+        "value": args.steps / r["elapsed"], "unit": "EM iters/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": arithmetic_type(r["variant"]), "data": "synthetic (configs.make_shape)",
+        "config": {"workload": f"diag-cov GMM EM N={N} K={K} d={d} fp32"
+                               + (" (all components within 0.02)" if args.overlap else ""),
+                   "N": N, "K": K, "d": d, "kernel_variant": r["variant"]},
+        "roofline": dominant_roofline(cfg, r["variant"], r["kernels"]),
+        "timing": {"profiled_run_ms_per_step": r["elapsed_profiled"] * 1e3 / args.steps,
+                   "kernels_ms_per_launch": {k: v["ms_avg"] for k, v in r["kernels"].items()}},
+        "counts": r["counts"], "workspace_bytes": r["workspace_bytes"],
+        "dense_from_iteration": r["dense_from_iteration"],
+        "ll_first": r["ll_first"], "ll_last": r["ll_last"],
+    }
 
 
 def main():
@@ -428,6 +462,10 @@ def main():
         if rank == 0:
             print(json.dumps(run_stream(args.config, args.steps, args.warmup, args.stream_chunk,
                                         args.variant)), flush=True)
+        return
+    if args.shape:
+        if rank == 0:
+            print(json.dumps(measure_shape(args)), flush=True)
         return
     with_cpu = rank == 0 and not args.no_cpu_baseline
     cids = [int(c) for c in args.configs.split(",") if c.strip()]

@@ -31,6 +31,7 @@ SIGNATURES = {
                                ctypes.POINTER(_Z)], _I),
     "fgmm_workspace_bytes": ([_L, _I, _I, _I], _Z),
     "fgmm_em_fused_workspace_bytes": ([_L, _I, _I, _I], _Z),
+    "fgmm_em_fit_switch_iteration": ([], _I),
     "fgmm_em_fused": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _P, _P, _Z, _P], _I),
     "fgmm_em_fused_noalloc_max_bytes": ([], _Z),
     "fgmm_em_fused_noalloc": ([_P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P, _P, _P], _I),

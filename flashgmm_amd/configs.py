@@ -106,3 +106,26 @@ def make_problem(cid: int, N: int | None = None):
     var0 = np.ones((K, d), dtype=np.float32)
     log_pi0 = np.full(K, -math.log(K), dtype=np.float32)
     return X, mu0, var0, log_pi0
+
+
+def make_shape(N: int, K: int, d: int, overlap: bool = False, seed: int = 7):
+    """A seeded problem of any shape, for measurements beyond the five
+    configurations (same conventions as :func:`make_problem`: C2's mean and
+    standard-deviation ranges, equal weights, initial means = K data points,
+    unit variances).  ``overlap``: all K true means within 0.02 of one centre
+    (per coordinate), so every component lies inside every point's exact
+    window -- the sparse variant's worst case, where each point's list
+    overflows and the dense fp64 pass takes it."""
+    rng = np.random.default_rng(seed)
+    if overlap:
+        mu_true = rng.uniform(-5.0, 5.0, size=(1, d)) + 0.02 * rng.standard_normal((K, d))
+    else:
+        mu_true = rng.uniform(-5.0, 5.0, size=(K, d))
+    sd = rng.uniform(0.5, 1.5, size=(K, d))
+    z = rng.integers(0, K, size=N)
+    X = np.ascontiguousarray(mu_true[z] + sd[z] * rng.standard_normal((N, d)), dtype=np.float32)
+    idx = rng.choice(N, size=K, replace=False)
+    mu0 = np.ascontiguousarray(X[idx])
+    var0 = np.ones((K, d), dtype=np.float32)
+    log_pi0 = np.full(K, -math.log(K), dtype=np.float32)
+    return X, mu0, var0, log_pi0

@@ -743,6 +743,54 @@ int fgmm_m_step_update(const float* n_k, const float* s_k, const float* sq_k, lo
   return check_hip(launch_mstep(g, n_k, s_k, sq_k, mu, var, log_pi, s), "M-step");
 }
 
+// The device loop's fallback for data the sparse variant handles badly: when
+// most points' lists overflow (heavily overlapping components, where every
+// pair lies in the exact window and every point takes the dense pass
+// anyway), the fp64 matrix-core variant is several times faster.  Its
+// geometry is fitted into the caller's workspace by using fewer point chunks
+// (at least ceil(N / 16384), which keeps each chunk within the fp32 sum's
+// bound).
+static bool dense_geom_within(long N, int K, int d, size_t ws_bytes, Geom* out) {
+  Geom g = make_geom(N, K, d, kMfma);
+  const long min_chunks = (N + 16383) / 16384;
+  long S = g.p2_chunks;
+  while (make_layout(g).total > ws_bytes) {
+    if (S <= min_chunks) return false;
+    S = std::max<long>(min_chunks, S * 3 / 4);
+    const long chunk = round_up_l((N + S - 1) / S, 64);
+    g.p2_chunk = chunk;
+    g.p2_chunks = (int)((N + chunk - 1) / chunk);
+  }
+  *out = g;
+  return true;
+}
+
+// Per host thread: a pinned word the overflow count is copied into, on the
+// device it was made for, and the iteration of the last fgmm_em_fit call's
+// switch to the dense variant (-1: none).
+struct FitProbe {
+  int* host = nullptr;
+  int device = -1;
+};
+static thread_local FitProbe t_probe;
+static thread_local int t_switched = -1;
+
+static int* fit_probe_word() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if (t_probe.host == nullptr) {
+    if (hipHostMalloc(reinterpret_cast<void**>(&t_probe.host), sizeof(int),
+                      hipHostMallocDefault) != hipSuccess) {
+      t_probe.host = nullptr;
+      return nullptr;
+    }
+    t_probe.device = dev;
+  }
+  return t_probe.host;
+}
+
+int fgmm_em_fit_switch_iteration(void) { return t_switched; }
+
 int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float* log_pi0,
                 long N, int K, int d, int iters, int variant, float* mu_out, float* var_out,
                 float* log_pi_out, double* ll_traj, void* ws, size_t ws_bytes,
@@ -771,6 +819,11 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
     }
     return FGMM_OK;
   }
+  // auto-selected sparse: after the second iteration (when more than two
+  // follow), one wait for the overflow count decides whether the rest runs
+  // on the dense fp64 matrix cores (more than half the points overflowed)
+  const bool adapt = variant == kAuto && g.variant == kSparse;
+  t_switched = -1;
   if ((rc = run_precompute(g, mu0, var0, log_pi0, w, s))) return rc;
   for (int it = 0; it < iters; it++) {
     if ((rc = run_pass1(g, X, w, nullptr, s))) return rc;
@@ -779,6 +832,23 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
     // coefficients the next iteration's passes read
     rc = run_reduce(g, X, w, mu_out, var_out, log_pi_out, w.params, w.bias, ll_traj + it, s);
     if (rc) return rc;
+    if (adapt && it == 1 && iters > 3) {
+      int* word = fit_probe_word();
+      Geom g2;
+      if (word != nullptr && dense_geom_within(N, K, d, ws_bytes, &g2)) {
+        rc = check_hip(hipMemcpyAsync(word, w.sp.nov, sizeof(int), hipMemcpyDeviceToHost, s),
+                       "overflow count read-back");
+        if (rc) return rc;
+        if ((rc = check_hip(hipStreamSynchronize(s), "overflow count read-back"))) return rc;
+        if (2L * *word > N) {
+          const WsLayout L2 = make_layout(g2);
+          g = g2;
+          w = carve(g, ws, L2);
+          if ((rc = run_precompute(g, mu_out, var_out, log_pi_out, w, s))) return rc;
+          t_switched = it + 1;
+        }
+      }
+    }
   }
   return FGMM_OK;
 }

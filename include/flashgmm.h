@@ -172,13 +172,27 @@ int fgmm_m_step_update(const float* n_k, const float* s_k, const float* sq_k,
  * DEVICE pointer to `iters` doubles) = mean_n log_normalizer under the
  * parameters entering iteration it -- the quantity NativeFlashGMM.fit
  * records per iteration (flash_gmm/native_wrapper.py:128-137) without its
- * per-iteration host synchronisation.  No early stop (tol = 0).
+ * per-iteration host synchronisation (one stream synchronisation after the
+ * second iteration when FGMM_VARIANT_AUTO selected the sparse variant and
+ * iters > 3: see fgmm_em_fit_switch_iteration).  No early stop (tol = 0).
  * mu0/var0/log_pi0 may alias mu_out/var_out/log_pi_out.
  */
 int fgmm_em_fit(const float* X, const float* mu0, const float* var0,
                 const float* log_pi0, long N, int K, int d, int iters, int variant,
                 float* mu_out, float* var_out, float* log_pi_out, double* ll_traj,
                 void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Diagnostic (host-only): the iteration from which the last fgmm_em_fit call
+ * on this host thread ran the fp64 matrix-core variant instead of an
+ * automatically selected sparse one, or -1.  With FGMM_VARIANT_AUTO and more
+ * than three iterations, fgmm_em_fit reads back the number of points whose
+ * pair lists overflowed in the second iteration (one stream synchronisation)
+ * and, when they are more than half of N, runs the remaining iterations on
+ * the dense kernels within the same workspace.  No counterpart in the
+ * reference.
+ */
+int fgmm_em_fit_switch_iteration(void);
 
 /*
  * Gamma-returning E-step on the flash schedule: Pass 1 (log-normalizer), then

@@ -152,11 +152,14 @@ def test_ll_trajectory_full_size(cuda, cid):
     assert (ref["N"], ref["K"], ref["d"]) == X.shape[:1] + mu.shape
     t = to_dev(cuda, X, mu, var, lp)
     traj_ref = np.array(ref["ll"])
-    for variant in variants_for(mu.shape[0], mu.shape[1]):
+    from flashgmm_amd import _lib
+    for variant in variants_for(mu.shape[0], mu.shape[1]) + ["auto"]:
         print(f"[case] full trajectory C{cid} iters={ref['iters']} variant={variant}", flush=True)
         _, _, _, traj = C.em_fit(*t, ref["iters"], variant=variant)
         e = np.abs(traj.cpu().numpy() - traj_ref) / np.abs(traj_ref)
         assert e.max() <= 1e-4, f"C{cid} {variant}: trajectory rel err {e.max():.3e} at it {e.argmax()}"
+        if variant == "auto":   # the benchmark configurations never leave their variant
+            assert _lib.load().fgmm_em_fit_switch_iteration() == -1
 
 
 # Reduced-size trajectories against the live oracle.  C4 is not reduced: at
@@ -175,6 +178,35 @@ def test_ll_trajectory(cuda, cid, N, iters):
         traj = traj.cpu().numpy()
         e = np.abs(traj - traj_ref) / np.abs(traj_ref)
         assert e.max() <= 1e-4, f"C{cid} {variant}: trajectory rel err {e.max():.3e} at it {e.argmax()}"
+
+
+def test_device_loop_falls_back_on_overlapping_components(cuda):
+    """All 256 components within 0.02 of one centre: every pair lies in each
+    point's exact window and every point's list overflows, the sparse
+    variant's worst case.  With variant auto the device loop reads the
+    overflow count after the second iteration and runs the rest on the fp64
+    matrix cores (fgmm_em_fit_switch_iteration() == 2); the trajectory meets
+    the fp64 oracle's to 1e-4 either way, a forced sparse run does not
+    switch, and a run of three iterations does not check."""
+    import torch
+    from flashgmm_amd import _lib
+    from flashgmm_amd import flash_gmm_native as C
+    from flashgmm_amd.configs import make_shape
+    X, mu, var, lp = make_shape(16384, 256, 32, overlap=True)
+    iters = 8
+    traj_ref, *_ = O.c_fit(X, mu, var, lp, iters)
+    t = to_dev(cuda, X, mu, var, lp)
+    lib = _lib.load()
+    for variant, switch in (("auto", 2), ("sparse", -1), ("mfma", -1)):
+        print(f"[case] overlapping components variant={variant}", flush=True)
+        _, _, _, traj = C.em_fit(*t, iters, variant=variant)
+        torch.cuda.synchronize()
+        assert lib.fgmm_em_fit_switch_iteration() == switch, variant
+        e = np.abs(traj.cpu().numpy() - traj_ref) / np.abs(traj_ref)
+        print(f"[parity] overlapping {variant}: trajectory rel err {e.max():.2e}", flush=True)
+        assert e.max() <= 1e-4, f"{variant}: trajectory rel err {e.max():.3e} at it {e.argmax()}"
+    C.em_fit(*t, 3)
+    assert lib.fgmm_em_fit_switch_iteration() == -1
 
 
 def test_driver_matches_device_loop(cuda):
