@@ -765,28 +765,18 @@ static bool dense_geom_within(long N, int K, int d, size_t ws_bytes, Geom* out) 
   return true;
 }
 
-// Per host thread: a pinned word the overflow count is copied into, on the
-// device it was made for, and the iteration of the last fgmm_em_fit call's
-// switch to the dense variant (-1: none).
-struct FitProbe {
-  int* host = nullptr;
-  int device = -1;
-};
-static thread_local FitProbe t_probe;
+// Per host thread: a pinned word the overflow count is copied into
+// (allocated on first use, kept until the process ends), and the iteration
+// of the last fgmm_em_fit call's switch to the dense variant (-1: none).
+static thread_local int* t_probe_word = nullptr;
 static thread_local int t_switched = -1;
 
 static int* fit_probe_word() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  if (t_probe.host == nullptr) {
-    if (hipHostMalloc(reinterpret_cast<void**>(&t_probe.host), sizeof(int),
-                      hipHostMallocDefault) != hipSuccess) {
-      t_probe.host = nullptr;
-      return nullptr;
-    }
-    t_probe.device = dev;
-  }
-  return t_probe.host;
+  if (t_probe_word == nullptr &&
+      hipHostMalloc(reinterpret_cast<void**>(&t_probe_word), sizeof(int),
+                    hipHostMallocDefault) != hipSuccess)
+    t_probe_word = nullptr;
+  return t_probe_word;
 }
 
 int fgmm_em_fit_switch_iteration(void) { return t_switched; }
@@ -821,8 +811,12 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
   }
   // auto-selected sparse: after the second iteration (when more than two
   // follow), one wait for the overflow count decides whether the rest runs
-  // on the dense fp64 matrix cores (more than half the points overflowed)
-  const bool adapt = variant == kAuto && g.variant == kSparse;
+  // on the dense fp64 matrix cores (more than half the points overflowed).
+  // Not while the stream is being captured, where a wait is not allowed.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const bool adapt = variant == kAuto && g.variant == kSparse &&
+                     hipStreamIsCapturing(s, &cap) == hipSuccess &&
+                     cap == hipStreamCaptureStatusNone;
   t_switched = -1;
   if ((rc = run_precompute(g, mu0, var0, log_pi0, w, s))) return rc;
   for (int it = 0; it < iters; it++) {

@@ -185,8 +185,9 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0,
 /*
  * Diagnostic (host-only): the iteration from which the last fgmm_em_fit call
  * on this host thread ran the fp64 matrix-core variant instead of an
- * automatically selected sparse one, or -1.  With FGMM_VARIANT_AUTO and more
- * than three iterations, fgmm_em_fit reads back the number of points whose
+ * automatically selected sparse one, or -1.  With FGMM_VARIANT_AUTO, more
+ * than three iterations and a stream that is not being captured into a
+ * graph, fgmm_em_fit reads back the number of points whose
  * pair lists overflowed in the second iteration (one stream synchronisation)
  * and, when they are more than half of N, runs the remaining iterations on
  * the dense kernels within the same workspace.  No counterpart in the

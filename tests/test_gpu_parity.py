@@ -209,6 +209,40 @@ def test_device_loop_falls_back_on_overlapping_components(cuda):
     assert lib.fgmm_em_fit_switch_iteration() == -1
 
 
+def test_device_loop_under_graph_capture(cuda):
+    """fgmm_em_fit captured into a HIP graph (torch.cuda.graph) on the
+    overlapping components above: a wait is not allowed under capture, so the
+    overflow read-back is skipped and the graph runs the sparse variant
+    throughout.  Three replays, with eager calls and synchronisations between
+    them, each equal the eager forced-sparse run bit for bit."""
+    import torch
+    from flashgmm_amd import _lib
+    from flashgmm_amd import flash_gmm_native as C
+    from flashgmm_amd.configs import make_shape
+    X, mu, var, lp = make_shape(16384, 256, 32, overlap=True)
+    t = to_dev(cuda, X, mu, var, lp)
+    ref = C.em_fit(*t, 6, variant="sparse")
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # warm-up on the capture's side stream (workspace)
+        C.em_fit(*t, 6)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    print("[case] device loop under graph capture", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = C.em_fit(*t, 6)
+    assert _lib.load().fgmm_em_fit_switch_iteration() == -1
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(out, ref):
+            assert torch.equal(a, b), f"replay {rep}"
+        C.em_fit(*t, 2)
+        torch.cuda.synchronize()
+
+
 def test_driver_matches_device_loop(cuda):
     """NativeFlashGMM.fit (per-call path, host sync per iteration) and
     fit_device (one device loop) record the same history."""
