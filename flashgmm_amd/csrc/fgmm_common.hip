@@ -227,7 +227,10 @@ hipError_t launch_precompute(const Geom& g, const float* mu, const float* var,
 // and flags the component when any bound exceeds kX32Guard (a tenth of the
 // 1e-5 parity bar); its statistics are then recomputed exactly.
 constexpr double kX32Guard = 1e-6;
-constexpr int kReduceThreadsMax = 256;   // the sparse reductions run this many threads
+// Threads of the sparse reductions' workgroups (one per component): 512 up to
+// 512 components, 256 beyond, where more workgroups than CUs share the GPU
+constexpr int kReduceThreadsMax = 512;
+inline int reduce_threads(int Kp) { return Kp <= 512 ? 512 : 256; }
 
 __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
                               int S, int stat_w, const double* __restrict__ part,
@@ -513,7 +516,7 @@ hipError_t launch_reduce_sparse(const Geom& g, const double* part, int S, const 
       (stage == kReduceFlagged && nflag == nullptr) || g.sp_ov_cap < 1 || g.sp_rows_fl < 16)
     return hipErrorInvalidValue;
   const int blocks = (params_next != nullptr || stage == kReduceFlagging) ? g.Kp : g.K;
-  hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(kReduceThreadsMax), 0, s, g.variant, g.N,
+  hipLaunchKernelGGL(reduce_kernel, dim3(blocks), dim3(reduce_threads(g.Kp)), 0, s, g.variant, g.N,
                      g.K, g.Kp, g.d, g.dp, S, g.stat_w, part, lnsum, g.p1_blocks, nullptr,
                      nullptr, nullptr, new_mu, new_var, new_log_pi, params_next, bias_next,
                      ll_out, 0, stage, flag, part2, ndyn, chunk2 < 1 ? 1L : chunk2, pstart,
