@@ -377,6 +377,11 @@ EDGE = {
     "K33_N1025": dict(N=1025, K=33, d=64),
     # Kp > 2048: the sparse chunk sort takes its bitonic path
     "K3000": dict(N=4096, K=3000, d=32),
+    # the sparse variant's largest K at its largest d (top-level scan and
+    # chunk sort at their LDS maxima)
+    "K8192_d128": dict(N=2048, K=8192, d=128),
+    # sparse with ragged N, K and d
+    "K200_N1001_d100": dict(N=1001, K=200, d=100),
 }
 
 
@@ -391,7 +396,8 @@ def test_edge_shapes(cuda, name):
     mu = (mu + rng.normal(0, 0.1, mu.shape)).astype(np.float32)
     var = rng.uniform(0.5, 2.0, (K, d)).astype(np.float32)
     lp = np.log(rng.dirichlet(np.ones(K))).astype(np.float32)
-    ref = O.np_em_fused(X, mu, var, lp)
+    # the numpy restatement for small shapes, the C one (OpenMP) for large K
+    ref = O.np_em_fused(X, mu, var, lp) if N * K <= 1 << 22 else O.c_em_fused(X, mu, var, lp)
     t = to_dev(cuda, X, mu, var, lp)
     for variant in variants_for(K, d):
         print(f"[case] edge {name} variant={variant}", flush=True)
