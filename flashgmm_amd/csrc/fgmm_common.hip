@@ -325,18 +325,18 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
         const double* p2 = part2 + (size_t)k * row + 2 * dp;
         for (int s = threadIdx.x; s < S2; s += blockDim.x) v5[0] += p2[(size_t)s * kstride];
       }
-      if (dmass != nullptr) {
+      if (dmass != nullptr) {   // eight bounds in flight per thread, added in order
         const float* dm = dmass + (size_t)k * nblk;
+        const int bd = blockDim.x;
         int b = threadIdx.x;
-        for (; b + 3 * (int)blockDim.x < nblk; b += 4 * blockDim.x) {
-          const float f0 = dm[b], f1 = dm[b + blockDim.x], f2 = dm[b + 2 * blockDim.x],
-                      f3 = dm[b + 3 * blockDim.x];
-          v5[4] += (double)f0;
-          v5[4] += (double)f1;
-          v5[4] += (double)f2;
-          v5[4] += (double)f3;
+        for (; b + 7 * bd < nblk; b += 8 * bd) {
+          float f[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) f[u] = dm[b + u * bd];
+#pragma unroll
+          for (int u = 0; u < 8; u++) v5[4] += (double)f[u];
         }
-        for (; b < nblk; b += blockDim.x) v5[4] += (double)dm[b];
+        for (; b < nblk; b += bd) v5[4] += (double)dm[b];
       }
       block_sum_f64_n<5>(v5, redn);
       t = v5[0];

@@ -115,7 +115,21 @@ struct X32Ws {
   float* dmass;        // [Kp][p1_blocks] bound on the unlisted responsibility mass
 };
 constexpr int kX32Slots = 16;   // exact (component, gamma) slots per point
-constexpr int kX1Waves = 8;     // Pass-1 wavefronts per workgroup of the x32 family (16 points each)
+// Pass-1 wavefronts per workgroup of the x32 family (16 points each): the
+// sparse variant's emit mode runs 4 up to 512 components, so that two
+// workgroups share a CU and one's end-of-sweep exact evaluation overlaps the
+// other's sweep (C3 Pass 1 -7 %, C5's heavy second iteration -1 ms); 8
+// otherwise, where the sweep is long and twice the per-workgroup bounds
+// would only cost the reduction more reads.
+__host__ __device__ constexpr int x1_waves(int variant, int Kp) {
+  return (variant == kSparse && Kp <= 512) ? 4 : 8;
+}
+// Coefficient tiles held in LDS by one Pass-1 workgroup: two (the next tile
+// stored while the current one is read), or one where two 4-wave workgroups
+// would otherwise not share a CU (dp > 64)
+__host__ __device__ constexpr int x1_tile_bufs(int dp, int waves) {
+  return (waves == 8 || dp <= 64) ? 2 : 1;
+}
 
 // Sparse variant.  Pass 1 lists every pair it evaluates exactly (those whose
 // fp32 upper bound reaches within 40 bits of the point's best lower bound);

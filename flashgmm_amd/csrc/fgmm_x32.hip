@@ -48,9 +48,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kW1 = kX1Waves;           // Pass 1 wavefronts per workgroup
-constexpr int kPts1 = 16 * kW1;         // Pass 1 points per workgroup
-constexpr int kThr1 = 64 * kW1;
 constexpr int kSub1 = 2;                // 16-component subtiles per LDS tile
 constexpr int kPendL = 16;              // pending list length per lane (>= 8 per tile)
 constexpr int kW2 = 4;                  // Pass 2 wavefronts (16 components each)
@@ -150,15 +147,17 @@ __device__ inline void load_quarter32(const float* __restrict__ X, long n, long 
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1.  Workgroup = 8 wavefronts x 16 points, coefficient tiles of 32
-// components double-buffered in LDS (as the fp64 variant).  The fp32
+// Pass 1.  Workgroup = W wavefronts x 16 points (W = x1_waves: 8, or 4 in
+// the sparse variant up to 512 components), coefficient tiles of 32
+// components double-buffered in LDS (single-buffered at W = 4, d_p > 64, so
+// that two workgroups fit one CU).  The fp32
 // accumulator of the 16x16x4 instruction gives lane (g, c) components 4g+r
 // (r = 0..3) of each subtile for point c; the same lane holds features
 // [gQ, (g+1)Q) of point c.  Behind the two coefficient tiles LDS holds the
-// lanes' pending lists, entry i of thread t at i*512 + t (conflict-free).
+// lanes' pending lists, entry i of thread t at i*64W + t (conflict-free).
 // ---------------------------------------------------------------------------
-template <int DP, bool VEC, int MODE>
-__global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
+template <int DP, bool VEC, int MODE, int W>
+__global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
     const float* __restrict__ X, long N, int d, int Kp, const float* __restrict__ P32,
     const float* __restrict__ bias32, const float* __restrict__ Z32,
     const double* __restrict__ V2, const double* __restrict__ b64,
@@ -167,6 +166,7 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
     float* __restrict__ cg, unsigned short* __restrict__ pk, double* __restrict__ pv,
     int* __restrict__ pcnt, int pC, float* __restrict__ dmass) {
   constexpr bool SLOTS = MODE == kX1Slots, EMIT = MODE == kX1Emit;
+  constexpr int kW1 = W, kPts1 = 16 * W, kThr1 = 64 * W;   // wavefronts, points, threads
   constexpr float kWinP1 = kWin;
   // EMIT (sparse variant): the sweep runs on bf16 matrix cores with split
   // operands (x32_err_c_bf); features in octet order, padded to DPB
@@ -179,11 +179,12 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
   constexpr int TV4 = TILE / 4;                         // float4 per tile
   constexpr int PER = (TV4 + kThr1 - 1) / kThr1;
   constexpr float Wslope = (float)(2.0 * (BF ? x32_err_c_bf(DPB) : x32_err_c(DP)));
-  extern __shared__ float smemf[];                      // [2][TILE], int2 [kPendL][512]
+  extern __shared__ float smemf[];                      // [NBUF][TILE], int2 [kPendL][64W]
   __shared__ float sB[2][16 * kSub1], sZ[2][16 * kSub1];
   __shared__ double red[kW1];
   __shared__ float dsh[2][kW1][16 * kSub1];   // EMIT: per-wave dropped-mass bounds of a tile
-  int2* plist = reinterpret_cast<int2*>(smemf + 2 * TILE);
+  constexpr int NBUF = x1_tile_bufs(DP, W);
+  int2* plist = reinterpret_cast<int2*>(smemf + NBUF * TILE);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -233,9 +234,11 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
       preZ = Z32[(t) * 16 * kSub1 + tid];                                             \
     }                                                                                 \
   }
+// tile into tile buffer (buf) when there are two, else buffer 0; the bias
+// and bound constants always into their buffer (buf)
 #define FGMM_X1_LSTORE(buf)                                                           \
   {                                                                                   \
-    f32x4* dst_ = reinterpret_cast<f32x4*>(smemf + (buf) * TILE);                     \
+    f32x4* dst_ = reinterpret_cast<f32x4*>(smemf + (NBUF == 2 ? (buf) : 0) * TILE);  \
     _Pragma("unroll") for (int i_ = 0; i_ < PER; i_++) {                              \
       const int q_ = tid + i_ * kThr1;                                                \
       if (TV4 % kThr1 == 0 || q_ < TV4) dst_[q_] = pre[i_];                           \
@@ -440,7 +443,7 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
   for (int t = 0; t < ntiles; t++) {
     const int buf = t & 1;
     if (t + 1 < ntiles) FGMM_X1_GLOAD(t + 1)
-    const float* sP = smemf + buf * TILE;
+    const float* sP = smemf + (NBUF == 2 ? buf : 0) * TILE;
     // q: x^2 part (no bias), l: bias + x part, one pair per subtile
     f32x4 q0 = f32x4{0.f, 0.f, 0.f, 0.f}, q1 = q0, l0, l1;
 #pragma unroll
@@ -549,7 +552,10 @@ __global__ __launch_bounds__(kThr1, 2) void pass1_x32_kernel(
         }
       }
     }
-    if (t + 1 < ntiles) FGMM_X1_LSTORE(buf ^ 1)
+    if (t + 1 < ntiles) {
+      if (NBUF == 1) __syncthreads();   // one tile buffer: every wavefront has read it
+      FGMM_X1_LSTORE(buf ^ 1)
+    }
     __syncthreads();
   }
 #undef FGMM_X1_GLOAD
@@ -973,19 +979,19 @@ __global__ __launch_bounds__(256) void x32_fix_kernel(
   }
 }
 
-template <int DP, bool VEC, int MODE>
+template <int DP, bool VEC, int MODE, int W>
 hipError_t x1_launch_mode(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                           float* ln_out, double* lnsum, hipStream_t s) {
-  constexpr size_t lds = 2 * (size_t)x1_tile_floats(DP, MODE) * sizeof(float) +
-                         (size_t)kPendL * kThr1 * sizeof(int2);
+  constexpr size_t lds = (size_t)x1_tile_bufs(DP, W) * x1_tile_floats(DP, MODE) * sizeof(float) +
+                         (size_t)kPendL * 64 * W * sizeof(int2);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)pass1_x32_kernel<DP, VEC, MODE>,
+    hipError_t e = hipFuncSetAttribute((const void*)pass1_x32_kernel<DP, VEC, MODE, W>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((pass1_x32_kernel<DP, VEC, MODE>), dim3(g.p1_blocks), dim3(kThr1), lds, s,
+  hipLaunchKernelGGL((pass1_x32_kernel<DP, VEC, MODE, W>), dim3(g.p1_blocks), dim3(64 * W), lds, s,
                      X, g.N, g.d, g.Kp, w.P32, w.bias32, w.Z32, w.V, w.b64, ln2, ln_out, lnsum,
                      w.m32, w.xm, w.ck, w.cg, w.pk, w.pv, w.pcnt, w.pC, w.dmass);
   return hipGetLastError();
@@ -996,14 +1002,20 @@ hipError_t x1_launch_mode(const Geom& g, const float* X, const X32Ws& w, double*
 template <int DP, bool VEC>
 hipError_t x1_launch(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                      float* ln_out, double* lnsum, hipStream_t s) {
-  if (w.ck != nullptr) return x1_launch_mode<DP, VEC, kX1Slots>(g, X, w, ln2, ln_out, lnsum, s);
+  static_assert(x1_waves(kX32, 1 << 20) == 8 && x1_waves(kMixed, 1) == 8,
+                "only the emit mode has a 4-wave instantiation");
+  if (w.ck != nullptr)
+    return x1_launch_mode<DP, VEC, kX1Slots, 8>(g, X, w, ln2, ln_out, lnsum, s);
   if (w.pk != nullptr) {
     if (w.pv == nullptr || w.pcnt == nullptr || w.xm == nullptr || w.dmass == nullptr ||
         w.pC < 1)
       return hipErrorInvalidValue;
-    return x1_launch_mode<DP, VEC, kX1Emit>(g, X, w, ln2, ln_out, lnsum, s);
+    // the host sized p1_blocks and dmass for this wave count
+    if (x1_waves(kSparse, g.Kp) == 4)
+      return x1_launch_mode<DP, VEC, kX1Emit, 4>(g, X, w, ln2, ln_out, lnsum, s);
+    return x1_launch_mode<DP, VEC, kX1Emit, 8>(g, X, w, ln2, ln_out, lnsum, s);
   }
-  return x1_launch_mode<DP, VEC, kX1Plain>(g, X, w, ln2, ln_out, lnsum, s);
+  return x1_launch_mode<DP, VEC, kX1Plain, 8>(g, X, w, ln2, ln_out, lnsum, s);
 }
 
 template <int DP, bool VEC>
