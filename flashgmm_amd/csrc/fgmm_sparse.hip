@@ -48,7 +48,6 @@ constexpr int kScanThreads = 1024;
 constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
-constexpr int kAccUnroll = 4;      // entries per lane group in flight
 constexpr int kPre = kSpCap;       // list entries per point requested ahead in the chunk sort:
                                    // all of them, so a long list costs no extra round trips
 constexpr int kSpCountMax = 2048;  // up to this Kp the chunk sort is a counting sort
@@ -411,134 +410,190 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// piece sums: L lanes per entry (lane j holds features 4j..4j+3), H = 256/L
-// entries side by side, kAccUnroll entries per lane group loaded before use
+// piece sums.  A piece's entries are taken 256 at a time, one per thread
+// (entry 4 * lane + wavefront of the round, so that a short piece still
+// spreads over the four wavefronts): a bound entry adds its weight times {1, max|x|, max x^2} to the thread's
+// error sums; each wavefront compacts its exact entries, in entry order,
+// into its own LDS slice (ballot and lane counts: no barrier) and gathers
+// their rows of X with lane groups of L lanes per row (lane j holds
+// features 4j..4j+3), GW = 64/L rows side by side, 16 rows per batch, so
+// that lanes are spent only on rows that exist.  One barrier per piece, for
+// the sums across lane groups (double-buffered by piece parity).  A barrier
+// waits for every outstanding load, so every load of a round is issued
+// after it: the next round's entries and the bound entries' max x^2 travel
+// with the rows.
 // ---------------------------------------------------------------------------
+constexpr int kWaveRows = 16;   // rows of X one wavefront requests per batch
+
+// fp64 sum over the wavefront in a fixed butterfly order (every lane gets it)
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 template <int L, bool VEC>
 __global__ __launch_bounds__(kT) void sp_piece_kernel(
-    int d, int dp, int stat_w, const int4* __restrict__ pinfo, const int* __restrict__ nov,
+    int d, int dp, int stat_w, const int4* pinfo, const int* __restrict__ nov,
     const int2* __restrict__ sorted,
     const float* __restrict__ X, const float* __restrict__ xm, double* __restrict__ prow) {
-  constexpr int H = kT / L;
-  __shared__ double sa[H][4 * L], sb[H][4 * L];
-  __shared__ double sn[H][4];
-  const int tid = threadIdx.x;
-  const int j = tid % L, h = tid / L;
+  constexpr int H = kT / L;           // lane groups of the workgroup
+  constexpr int GW = 64 / L;          // lane groups of a wavefront
+  constexpr int U = kWaveRows / GW;   // rows per lane group in flight
+  static_assert(U >= 1 && U * GW == kWaveRows, "batch shape");
+  constexpr int NW = kT / 64;
+  __shared__ double sa[2][H][4 * L], sb[2][H][4 * L];
+  __shared__ double sk[2][H];         // per lane group: sum of exact weights
+  __shared__ double se[2][NW][3];     // per wavefront: bound sums
+  // each wavefront's exact entries of a round, then zeros: slots past the
+  // exact entries are cleared every round and 64..79 once, so that a batch
+  // reads its 16 slots without a bounds test (a test makes each LDS read a
+  // branch of its own with a wait)
+  __shared__ int2 cl[NW][64 + kWaveRows];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int j = tid % L, h = tid / L, gw = lane / L;
+  const int eo = lane * NW + wv;   // this thread's entry within a round
   const int j0 = 4 * j;
   const int npiece = nov[1];
-  constexpr int kStep = H * kAccUnroll;
   const int G = (int)gridDim.x;
-  // Pieces are pipelined: the entry ranges are loaded two pieces ahead and
-  // the next piece's first batch of entries while this piece is summed.
-  // pinfo rows past npiece are not written: an absent piece reads row 0
-  // (always inside the capacity) and takes the empty range (0, 0) instead,
-  // a select of values, so the load stays a global load.  Weight 0 past a
-  // piece has no effect.
+  // Pieces are pipelined: the entry ranges are loaded two pieces ahead, and
+  // each round's entries (the next round's, or the next piece's first) with
+  // the current round's rows of X.  pinfo rows past npiece are not written:
+  // an absent piece reads row 0 (always inside the capacity) and takes the
+  // empty range (0, 0) instead, a select of values, so the load stays a
+  // global load.  Only the entry range (x, y) of a record is read.  pinfo is
+  // not declared restrict, so that the records are fetched by vector loads
+  // (the row stores might alias them): a scalar load would be waited for by
+  // the first LDS read after it, the same counter; its value is made
+  // uniform again where it is used.
   auto piece_at = [&](int i) {
-    const int4 v = pinfo[i < npiece ? i : 0];
-    return i < npiece ? v : make_int4(0, 0, 0, 0);
+    const int2 v = reinterpret_cast<const int2*>(pinfo)[2 * (i < npiece ? i : 0)];
+    return i < npiece ? v : make_int2(0, 0);
   };
-  int4 cur = piece_at(blockIdx.x);
-  int4 nxt = piece_at(blockIdx.x + G);
-  int2 en[kAccUnroll];
-#pragma unroll
-  for (int u = 0; u < kAccUnroll; u++) {
-    const int eu = cur.x + h + u * H;
-    en[u] = eu < cur.y ? sorted[eu] : make_int2(0, 0);
-  }
-  for (int pc = blockIdx.x; pc < npiece; pc += G) {
+  int2 cur = piece_at(blockIdx.x);
+  int2 nxt = piece_at(blockIdx.x + G);
+  int2 ent = cur.x + eo < cur.y ? sorted[cur.x + eo] : make_int2(0, 0);
+  if (lane < kWaveRows) cl[wv][64 + lane] = make_int2(0, 0);
+  int par = 0;
+  for (int pc = blockIdx.x; pc < npiece; pc += G, par ^= 1) {
     const int e0 = cur.x, e1 = cur.y;
-    const int4 after = piece_at(pc + 2 * G);
-    int2 enx[kAccUnroll];   // the next piece's first batch
-#pragma unroll
-    for (int u = 0; u < kAccUnroll; u++) {
-      const int eu = nxt.x + h + u * H;
-      enx[u] = eu < nxt.y ? sorted[eu] : make_int2(0, 0);
-    }
+    const int2 after = piece_at(pc + 2 * G);
     double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
     double nk = 0.0, eb = 0.0, es = 0.0, eq = 0.0;
-    // within a piece, the entries of the next batch are loaded while this
-    // batch's rows of X are in flight
-    for (int e = e0 + h; e < e1; e += kStep) {
-      int2 nx[kAccUnroll];
+    for (int r0 = e0; r0 < e1; r0 += kT) {
+      const float w = __int_as_float(ent.y);
+      const unsigned long long m = __ballot(w > 0.f);
+      const int pos = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+      const int nex = __popcll(m);
+      cl[wv][w > 0.f ? pos : nex + lane - pos] = w > 0.f ? ent : make_int2(0, 0);
+      // the slice is this wavefront's own: order its LDS writes before the
+      // reads below, no workgroup barrier
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // Every load below is unconditional, at an index that is always
+      // valid, its value selected afterwards: a load under a branch is
+      // compiled with a wait for it at the branch's end, which would take
+      // the loads of a batch one round trip at a time.
+      const int rn = r0 + kT;
+      const int en_at = rn < e1 ? rn + eo : nxt.x + eo;
+      const bool en_ok = en_at < (rn < e1 ? e1 : nxt.y);
+      const int2 entr = sorted[en_ok ? en_at : 0];
+      const int2 entn = en_ok ? entr : make_int2(0, 0);
+      const float x2r = xm[ent.x];   // a point index (0 past the piece)
+      const float x2b = w < 0.f ? x2r : 0.f;
+      for (int e = gw; e < nex; e += kWaveRows) {
+        int2 en[U];
+        float4 xv[U];
 #pragma unroll
-      for (int u = 0; u < kAccUnroll; u++) {
-        const int eu = e + kStep + u * H;
-        nx[u] = eu < e1 ? sorted[eu] : make_int2(0, 0);
-      }
-      float4 xv[kAccUnroll];
+        for (int u = 0; u < U; u++) en[u] = cl[wv][e + u * GW];   // e + u GW < 80
 #pragma unroll
-      for (int u = 0; u < kAccUnroll; u++) {
-        xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j0 < d && __int_as_float(en[u].y) > 0.f) {
-          const float* src = X + (size_t)en[u].x * d + j0;
+        for (int u = 0; u < U; u++) {
+          // past the list en[u] = (0, 0): row 0, weight 0
+          const float* row = X + (size_t)en[u].x * d;
+          float4 t;
           if (VEC) {
-            xv[u] = *reinterpret_cast<const float4*>(src);
+            t = *reinterpret_cast<const float4*>(row + (j0 < d ? j0 : 0));
           } else {
-            xv[u].x = src[0];
-            if (j0 + 1 < d) xv[u].y = src[1];
-            if (j0 + 2 < d) xv[u].z = src[2];
-            if (j0 + 3 < d) xv[u].w = src[3];
+            t.x = row[j0 < d ? j0 : 0];
+            t.y = row[j0 + 1 < d ? j0 + 1 : 0];
+            t.z = row[j0 + 2 < d ? j0 + 2 : 0];
+            t.w = row[j0 + 3 < d ? j0 + 3 : 0];
           }
+          const bool ok = j0 < d && __int_as_float(en[u].y) > 0.f;
+          xv[u].x = ok ? t.x : 0.f;
+          xv[u].y = ok && (VEC || j0 + 1 < d) ? t.y : 0.f;
+          xv[u].z = ok && (VEC || j0 + 2 < d) ? t.z : 0.f;
+          xv[u].w = ok && (VEC || j0 + 3 < d) ? t.w : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const double wx0 = (double)__int_as_float(en[u].y);   // 0 past the list
+          const double x4[4] = {(double)xv[u].x, (double)xv[u].y, (double)xv[u].z,
+                                (double)xv[u].w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const double wx = wx0 * x4[q];   // exact: 24-bit times 24-bit
+            a[q] += wx;
+            b[q] = fma(wx, x4[q], b[q]);
+          }
+          nk += wx0;
         }
       }
-#pragma unroll
-      for (int u = 0; u < kAccUnroll; u++) {
-        const double w = (double)__int_as_float(en[u].y);
-        if (w < 0.0) {   // bound entry: error columns only
-          if (j == 0) {
-            const double x2 = (double)xm[en[u].x];
-            eb -= w;
-            es -= w * sqrt(x2);
-            eq -= w * x2;
-          }
-          continue;
-        }
-        const double x4[4] = {(double)xv[u].x, (double)xv[u].y, (double)xv[u].z,
-                              (double)xv[u].w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const double wx = w * x4[q];   // exact: 24-bit times 24-bit
-          a[q] += wx;
-          b[q] = fma(wx, x4[q], b[q]);
-        }
-        nk += w;
+      if (w < 0.f) {   // bound entry: error columns only
+        const double wb = -(double)w, x2 = (double)x2b;
+        eb += wb;
+        es += wb * sqrt(x2);
+        eq += wb * x2;
       }
-#pragma unroll
-      for (int u = 0; u < kAccUnroll; u++) en[u] = nx[u];
+      // the slice is rewritten by the next round
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      ent = entn;
     }
+    if (e0 >= e1)   // an empty piece (none is made): keep the pipeline going
+      ent = nxt.x + eo < nxt.y ? sorted[nxt.x + eo] : make_int2(0, 0);
+    eb = wave_sum(eb);
+    es = wave_sum(es);
+    eq = wave_sum(eq);
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      sa[h][j0 + q] = a[q];
-      sb[h][j0 + q] = b[q];
+      sa[par][h][j0 + q] = a[q];
+      sb[par][h][j0 + q] = b[q];
     }
-    if (j == 0) {
-      sn[h][0] = nk;
-      sn[h][1] = eb;
-      sn[h][2] = es;
-      sn[h][3] = eq;
+    if (j == 0) sk[par][h] = nk;
+    if (lane == 0) {
+      se[par][wv][0] = eb;
+      se[par][wv][1] = es;
+      se[par][wv][2] = eq;
     }
+    // one barrier per piece: the next piece writes the other buffers, and
+    // every wavefront has passed this barrier (after its reads of them for
+    // the piece before) when any wavefront writes them again
     __syncthreads();
     double* row = prow + (size_t)pc * stat_w;
     for (int f = tid; f < d; f += kT) {
       double ta = 0.0, tb = 0.0;
       for (int i = 0; i < H; i++) {
-        ta += sa[i][f];
-        tb += sb[i][f];
+        ta += sa[par][i][f];
+        tb += sb[par][i][f];
       }
       row[f] = ta;
       row[dp + f] = tb;
     }
-    if (tid < 4) {
+    if (tid == 0) {
       double t = 0.0;
-      for (int i = 0; i < H; i++) t += sn[i][tid];
+      for (int i = 0; i < H; i++) t += sk[par][i];
+      row[2 * dp] = t;
+    } else if (tid >= 1 && tid <= 3) {
+      double t = 0.0;
+      for (int i = 0; i < NW; i++) t += se[par][i][tid - 1];
       row[2 * dp + tid] = t;
     }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kAccUnroll; u++) en[u] = enx[u];
     cur = nxt;
-    nxt = after;
+    nxt = make_int2(__builtin_amdgcn_readfirstlane(after.x), __builtin_amdgcn_readfirstlane(after.y));
   }
 }
 
