@@ -303,40 +303,70 @@ __global__ __launch_bounds__(256) void pass2_mfma_kernel(
 
   float4 pre[V4];
   double preL = 0.0;
+  long pre_t0 = 0;   // first point of the tile held in pre
+  // The next tile's loads are unconditional, at indices that are always
+  // valid (row p0 < p1 past the chunk, feature 0 past d), their values
+  // zeroed where they fall outside only when stored to LDS: a load under a
+  // branch, or a select right behind it, is compiled with a wait for it,
+  // which would take the tile's loads one round trip at a time.
   auto gload = [&](long t0) {
+    pre_t0 = t0;
+    // listed rows: all row indices (and the index of this thread's
+    // log-normalizer row) requested before any is used, one branch around
+    // them all; a wait for one load waits for every load before it, so
+    // the rows' loads are issued only after these
+    const bool okL = tid < kP2Tile && t0 + tid < p1;
+    long ri[V4], rl;
+    if (rowidx != nullptr) {
+      int rr[V4];
+#pragma unroll
+      for (int i = 0; i < V4; i++) {
+        const int row = (tid + i * 256) / (DP / 4);
+        rr[i] = rowidx[t0 + row < p1 ? t0 + row : p0];
+      }
+      const int rrl = rowidx[okL ? t0 + tid : p0];
+#pragma unroll
+      for (int i = 0; i < V4; i++) ri[i] = rr[i];
+      rl = rrl;
+    } else {
+#pragma unroll
+      for (int i = 0; i < V4; i++) {
+        const int row = (tid + i * 256) / (DP / 4);
+        ri[i] = t0 + row < p1 ? t0 + row : p0;
+      }
+      rl = okL ? t0 + tid : p0;
+    }
 #pragma unroll
     for (int i = 0; i < V4; i++) {
       const int idx = tid + i * 256;
       const int row = idx / (DP / 4), j = 4 * (idx - row * (DP / 4));
-      const long nn = t0 + row;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (nn < p1) {
-        const long ri = rowidx != nullptr ? (long)rowidx[nn] : nn;
-        const float* src = X + (size_t)ri * d + j;
-        if (VEC) {
-          if (j < d) v = *reinterpret_cast<const float4*>(src);
-        } else {
-          if (j < d) v.x = src[0];
-          if (j + 1 < d) v.y = src[1];
-          if (j + 2 < d) v.z = src[2];
-          if (j + 3 < d) v.w = src[3];
-        }
+      const float* src = X + (size_t)ri[i] * d;
+      if (VEC) {
+        pre[i] = *reinterpret_cast<const float4*>(src + (j < d ? j : 0));
+      } else {
+        pre[i].x = src[j < d ? j : 0];
+        pre[i].y = src[j + 1 < d ? j + 1 : 0];
+        pre[i].z = src[j + 2 < d ? j + 2 : 0];
+        pre[i].w = src[j + 3 < d ? j + 3 : 0];
       }
-      pre[i] = v;
     }
-    if (tid < kP2Tile) {   // gamma = 0 past the chunk
-      const long nn = t0 + tid;
-      preL = nn < p1 ? ln2[rowidx != nullptr ? (long)rowidx[nn] : nn] : INFINITY;
-    }
+    preL = ln2[rl];   // every thread: no branch around the load
   };
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < V4; i++) {
       const int idx = tid + i * 256;
       const int row = idx / (DP / 4), j = 4 * (idx - row * (DP / 4));
-      *reinterpret_cast<float4*>(&xs[buf][row * XS + j]) = pre[i];
+      const bool ok = pre_t0 + row < p1;
+      float4 v;
+      v.x = ok && j < d ? pre[i].x : 0.f;
+      v.y = ok && j + 1 < d ? pre[i].y : 0.f;
+      v.z = ok && j + 2 < d ? pre[i].z : 0.f;
+      v.w = ok && j + 3 < d ? pre[i].w : 0.f;
+      *reinterpret_cast<float4*>(&xs[buf][row * XS + j]) = v;
     }
-    if (tid < kP2Tile) ls[buf][tid] = preL;
+    // gamma = 0 past the chunk
+    if (tid < kP2Tile) ls[buf][tid] = pre_t0 + tid < p1 ? preL : INFINITY;
   };
 
   // distance product for one 16-point subtile: a0 (x^2 terms, with the
