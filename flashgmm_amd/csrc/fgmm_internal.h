@@ -108,8 +108,10 @@ struct X32Ws {
   float* cg;           // [N][kX32Slots] slot responsibilities (exact)
   int* flag;           // [Kp] components whose statistics are recomputed exactly
   // sparse variant: per-point pair lists written by Pass 1
-  unsigned short* pk;  // [N][pC] component (| kSpBound for a bound entry)
-  double* pv;          // [N][pC] exact ll2 (bound entry: upper bound of ll2)
+  // lists slot-major, entry i of point n at [i * N + n]: a chunk's first
+  // entries are contiguous, whatever the points' list lengths
+  unsigned short* pk;  // [pC][N] component (| kSpBound for a bound entry)
+  double* pv;          // [pC][N] exact ll2 (bound entry: upper bound of ll2)
   int* pcnt;           // [N] entries of the point (> pC: the list overflowed)
   int pC;
   float* dmass;        // [Kp][p1_blocks] bound on the unlisted responsibility mass

@@ -45,6 +45,7 @@ namespace {
 
 constexpr int kT = 256;            // threads of the chunk, scan-tile and piece kernels
 constexpr int kScanThreads = 1024;
+constexpr int kTopLen = 8;         // run lengths per thread of the top-level scan (Kp <= 8192)
 constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
@@ -123,8 +124,8 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     else m = c;
 #pragma unroll
     for (int i = 0; i < kPre; i++) {
-      kpre[i] = i < m ? (int)pk[(size_t)n * C + i] : 0;
-      vpre[i] = i < m ? pv[(size_t)n * C + i] : 0.0;
+      kpre[i] = i < m ? (int)pk[(size_t)i * N + n] : 0;
+      vpre[i] = i < m ? pv[(size_t)i * N + n] : 0.0;
     }
   }
   const int pos = block_excl_scan<kT>(m, sh, nullptr);
@@ -282,12 +283,26 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
   extern __shared__ int ps[];   // [Kp + 1] first piece of each component
   int* sg = ps + (Kp + 1);      // [Kp + 1] first entry of each component
   const int tid = threadIdx.x;
+  // every input is requested up front (one kernel, one round trip): the
+  // run lengths (Kp <= kTopLen x 1024), the first 1024 chunks' overflow
+  // counts and max x^2; indices are clamped and values selected, so no load
+  // sits under a branch
+  int lens[kTopLen];
+#pragma unroll
+  for (int u = 0; u < kTopLen; u++) {
+    const int k = u * kScanThreads + tid;
+    const int v = rowtot[k < Kp ? k : 0];
+    lens[u] = k < Kp ? v : 0;
+  }
+  const int oc0r = ocnt[tid < nchunk ? tid : 0];
+  const double xs0r = xsum[tid < nchunk ? tid : 0];
   int carry = 0;
-  for (int b = 0; b < Kp; b += kScanThreads) {
-    const int k = b + tid;
-    const int len = k < Kp ? rowtot[k] : 0;
+#pragma unroll
+  for (int u = 0; u < kTopLen; u++) {
+    if (u * kScanThreads >= Kp) break;
+    const int k = u * kScanThreads + tid;
     int tot;
-    const int ex = block_excl_scan<kScanThreads>(len, sh, &tot);
+    const int ex = block_excl_scan<kScanThreads>(lens[u], sh, &tot);
     if (k < Kp) {
       seg[k] = carry + ex;
       sg[k] = carry + ex;
@@ -300,10 +315,11 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
   int piece = kSpPiece;
   if ((total + piece - 1) / piece > budget) piece = (int)((total + budget - 1) / budget);
   int pcarry = 0;
-  for (int b = 0; b < Kp; b += kScanThreads) {
-    const int k = b + tid;
-    const int len = k < Kp ? rowtot[k] : 0;
-    const int np = (len + piece - 1) / piece;
+#pragma unroll
+  for (int u = 0; u < kTopLen; u++) {
+    if (u * kScanThreads >= Kp) break;
+    const int k = u * kScanThreads + tid;
+    const int np = (lens[u] + piece - 1) / piece;
     int ptot;
     const int pex = block_excl_scan<kScanThreads>(np, sh, &ptot);
     if (k < Kp) {
@@ -343,15 +359,15 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
   carry = 0;
   for (int b = 0; b < nchunk; b += kScanThreads) {
     const int i = b + tid;
-    const int v = i < nchunk ? ocnt[i] : 0;
+    const int v = b == 0 ? (i < nchunk ? oc0r : 0) : (i < nchunk ? ocnt[i] : 0);
     int tot;
     const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
     if (i < nchunk) ocnt[i] = carry + ex;
     carry += tot;
   }
   if (tid == 0) nov[0] = carry;
-  double a = 0.0;
-  for (int i = tid; i < nchunk; i += kScanThreads) a = fmax(a, xsum[i]);
+  double a = tid < nchunk ? xs0r : 0.0;
+  for (int i = tid + kScanThreads; i < nchunk; i += kScanThreads) a = fmax(a, xsum[i]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) a = fmax(a, __shfl_xor(a, off, 64));
   if ((tid & 63) == 0) d1[tid >> 6] = a;
@@ -378,26 +394,36 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
   extern __shared__ int rs[];   // [Kp] first index of each component in the chunk
   __shared__ int sh[kT];
   __shared__ int ovn[kSpPts];   // overflow points of the chunk, in order
+  __shared__ int kl[kT];        // the round's components, for the next thread's test
+  __shared__ int klast;         // the previous round's last component
   __shared__ int nov_sh;
   const int ch = blockIdx.x, tid = threadIdx.x;
   const long p0 = (long)ch * kSpPts;
   const int E = ecnt[ch];
-  const int2* in = blk + (size_t)ch * kSpChunkCap;
-  for (int i = tid; i < E; i += kT) {
-    const int k = in[i].x >> kPointBits;
-    if (i == 0 || (in[i - 1].x >> kPointBits) != k) rs[k] = i;
-  }
-  __syncthreads();
-  for (int i = tid; i < E; i += kT) {
-    const int2 e = in[i];
-    const int k = e.x >> kPointBits;
-    const long n = p0 + (e.x & (kSpPts - 1));
-    sorted[(size_t)seg[k] + off[(size_t)k * nchunk + ch] + (i - rs[k])] = make_int2((int)n, e.y);
-  }
-  // overflow points: lists longer than C, or cut by the chunk capacity
   const int cut = fcap[ch];
   const long np = p0 + tid;
-  const int f = (np < N) && (pcnt[np] > C || (tid >= cut && pcnt[np] > 0)) ? 1 : 0;
+  const int pn = pcnt[np < N ? np : 0];   // requested now, used after the entries
+  const int2* in = blk + (size_t)ch * kSpChunkCap;
+  // Entries are read once, 256 at a time: a run starts where the previous
+  // entry's component differs (the previous thread's entry, through LDS).
+  // The destinations are gathered after the round's run starts are known.
+  for (int i0 = 0; i0 < E; i0 += kT) {
+    const int i = i0 + tid;
+    const int2 e = in[i < E ? i : 0];
+    const int k = e.x >> kPointBits;
+    if (i < E) kl[tid] = k;
+    __syncthreads();
+    const int kp = tid > 0 ? kl[tid - 1] : (i0 > 0 ? klast : -1);
+    if (i < E && kp != k) rs[k] = i;
+    __syncthreads();
+    if (tid == kT - 1) klast = k;   // read by the next round after its first barrier
+    if (i < E) {
+      const long n = p0 + (e.x & (kSpPts - 1));
+      sorted[(size_t)seg[k] + off[(size_t)k * nchunk + ch] + (i - rs[k])] = make_int2((int)n, e.y);
+    }
+  }
+  // overflow points: lists longer than C, or cut by the chunk capacity
+  const int f = (np < N) && (pn > C || (tid >= cut && pn > 0)) ? 1 : 0;
   int tot;
   const int r = block_excl_scan<kT>(f, sh, &tot);
   if (f) ovn[r] = tid;
@@ -412,8 +438,8 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
 // ---------------------------------------------------------------------------
 // piece sums.  A piece's entries are taken 256 at a time, one per thread
 // (entry 4 * lane + wavefront of the round, so that a short piece still
-// spreads over the four wavefronts): a bound entry adds its weight times {1, max|x|, max x^2} to the thread's
-// error sums; each wavefront compacts its exact entries, in entry order,
+// spreads over the four wavefronts): a bound entry adds its weight times
+// {1, max|x|, max x^2} to the thread's error sums; each wavefront compacts its exact entries, in entry order,
 // into its own LDS slice (ballot and lane counts: no barrier) and gathers
 // their rows of X with lane groups of L lanes per row (lane j holds
 // features 4j..4j+3), GW = 64/L rows side by side, 16 rows per batch, so

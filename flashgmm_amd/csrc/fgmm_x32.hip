@@ -258,7 +258,7 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
   double sv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // largest exact pairs (slots)
   int sk4[4] = {-1, -1, -1, -1};
   int pc = 0;                             // EMIT: entries of this point's list so far
-  const size_t pbase = (size_t)(valid ? n : 0) * pC;
+  const long pidx = valid ? n : 0;   // EMIT: list entry i of the point at pk[i * N + pidx]
   // Exact evaluation of the live entries without slots: the entries of the
   // wavefront's 16 points form one queue (point-major, then lane group, then
   // list order) that the 16 lane columns share, so a round evaluates 16
@@ -327,9 +327,9 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
       if (g == 0 && 16 * r_ + c < T_) {                                               \
         reinterpret_cast<double*>(plist)[a_] = v_;                                    \
         if (EMIT && pcp_ + e_ < pC) {                                                 \
-          const size_t pb_ = (size_t)((long)blockIdx.x * kPts1 + wave * 16 + p_) * pC; \
-          pk[pb_ + pcp_ + e_] = (unsigned short)k_;                                   \
-          pv[pb_ + pcp_ + e_] = v_;                                                   \
+          const size_t pb_ = (size_t)(pcp_ + e_) * N + (long)blockIdx.x * kPts1 + wave * 16 + p_; \
+          pk[pb_] = (unsigned short)k_;                                               \
+          pv[pb_] = v_;                                                               \
         }                                                                             \
       }                                                                               \
     }                                                                                 \
@@ -372,8 +372,8 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
           live_++;                                                                    \
         } else if (h_ >= th_ - kSpKeep) {                                             \
           if (bp_ < pC) {                                                             \
-            pk[pbase + bp_] = (unsigned short)(e_.x | kSpBound);                      \
-            pv[pbase + bp_] = (double)h_;                                             \
+            pk[(size_t)bp_ * N + pidx] = (unsigned short)(e_.x | kSpBound);           \
+            pv[(size_t)bp_ * N + pidx] = (double)h_;                                  \
           }                                                                           \
           bp_++;                                                                      \
         }                                                                             \
