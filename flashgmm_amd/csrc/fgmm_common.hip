@@ -258,20 +258,61 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   const int k = blockIdx.x;
 
   if (stage == kReduceFlagged && (k >= K || flag[k] == 0)) return;
-  if (k == 0 && ll_out != nullptr) {
+  // The log-likelihood (block 0): the first 8 x blockDim terms are requested
+  // now and summed after the component's own loads, so that they cost block
+  // 0 no round trip of its own; the rest follows in batches of eight.  Per
+  // thread the terms are added in index order.  Every other block (and a
+  // call without terms: lnsum may be null, as for the standard M-step)
+  // reads the first element of part, the one input that is always there.
+  const bool do_ll = k == 0 && ll_out != nullptr && lnsum != nullptr && n_lnsum > 0;
+  const double* llsrc = do_ll ? lnsum : part;
+  double llv[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    const int j = (int)threadIdx.x + u * (int)blockDim.x;
+    llv[u] = llsrc[do_ll && j < n_lnsum ? j : 0];
+  }
+  auto ll_finish = [&]() {
+    if (!do_ll) return;
+    const int bd = blockDim.x;
     double t = 0.0;
-    for (int i = threadIdx.x; i < n_lnsum; i += blockDim.x) t += lnsum[i];
+#pragma unroll
+    for (int u = 0; u < 8; u++) t += (int)threadIdx.x + u * bd < n_lnsum ? llv[u] : 0.0;
+    for (int i = threadIdx.x + 8 * bd; i < n_lnsum; i += 8 * bd) {
+      double v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int j = i + u * bd;
+        const double x = lnsum[j < n_lnsum ? j : 0];
+        v[u] = j < n_lnsum ? x : 0.0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) t += v[u];
+    }
     t = block_sum_f64(t, red);
     if (threadIdx.x == 0) ll_out[0] = t / (double)N;
-  }
+  };
 
-  if (k >= K) {  // padding components only need coefficients for the next pass
+  if (k >= K) {  // padding components only need coefficients for the next pass (k > 0)
     if (stage == kReduceFlagging && threadIdx.x == 0) flag[k] = 0;
     if (P_next != nullptr)
       write_coeffs(variant, k, Kp, d, dp, nullptr, nullptr, 0.f, P_next, bias_next, red);
     return;
   }
 
+  // sparse, first stage: the first 8 x blockDim never-pending bounds are
+  // requested before anything else (they depend on k alone), at clamped
+  // indices with the values selected, so no load sits under a branch
+  float dm0[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (stage == kReduceFlagging && dmass != nullptr) {
+    const float* dm = dmass + (size_t)k * nblk;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int b = (int)threadIdx.x + u * (int)blockDim.x;
+      const float v = dm[b < nblk ? b : 0];
+      dm0[u] = b < nblk ? v : 0.f;
+    }
+  }
   const size_t row = (size_t)stat_w;
   const size_t kstride = (size_t)Kp * row;
   // sparse variant: partial rows of the dense pass over the overflow points
@@ -304,6 +345,23 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     pb = part + (size_t)(flag[k] - 1) * row;
     kst = (size_t)kact * row;
   }
+  // column sums (sparse variant, blockDim >= 2d): the rows are split over H
+  // groups of d threads and the H partial sums combined in order.  Each
+  // group's first eight rows are requested here, with the n_k columns
+  // below, at clamped rows (values selected when added), so the two loads
+  // share one round trip.
+  const int H = (variant == kSparse && (int)blockDim.x >= 2 * d) ? (int)blockDim.x / d : 1;
+  const int cj = (int)threadIdx.x % d, ch = (int)threadIdx.x / d;
+  double ca[8], cb[8];
+  if (H > 1) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const int s = ch + q * H;
+      const double* r = pb + (size_t)(s < Sk && ch < H ? s : 0) * kst;
+      ca[q] = r[cj];
+      cb[q] = r[dp + cj];
+    }
+  }
   {
     // n_k: chunk partials split across the block, merged in a fixed order
     double t = 0.0;
@@ -328,7 +386,9 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
       if (dmass != nullptr) {   // eight bounds in flight per thread, added in order
         const float* dm = dmass + (size_t)k * nblk;
         const int bd = blockDim.x;
-        int b = threadIdx.x;
+#pragma unroll
+        for (int u = 0; u < 8; u++) v5[4] += (double)dm0[u];   // 0 past nblk
+        int b = threadIdx.x + 8 * bd;
         for (; b + 7 * bd < nblk; b += 8 * bd) {
           float f[8];
 #pragma unroll
@@ -370,14 +430,18 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
   const double nk = nk_sh;
   const double inv = standard ? 1.0 / nk : 1.0 / (nk > 1e-8 ? nk : 1e-8);
   const double ncl = nk > 1e-8 ? nk : 1e-8;
-  // column sums (sparse variant, blockDim >= 2d): the rows are split over H
-  // groups of d threads and the H partial sums combined in order
-  const int H = (variant == kSparse && (int)blockDim.x >= 2 * d) ? (int)blockDim.x / d : 1;
   if (H > 1) {
-    const int jj = threadIdx.x % d, h = threadIdx.x / d;
+    const int jj = cj, h = ch;
     double a = 0.0, b = 0.0;
     if (h < H) {
-      int s = h;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {   // the first eight rows, requested above
+        if (h + q * H < Sk) {
+          a += ca[q];
+          b += cb[q];
+        }
+      }
+      int s = h + 8 * H;
       for (; s + 7 * H < Sk; s += 8 * H) {   // eight rows in flight, summed in order
         double va[8], vb[8];
 #pragma unroll
@@ -438,6 +502,7 @@ __global__ void reduce_kernel(int variant, long N, int K, int Kp, int d, int dp,
     }
   }
   __syncthreads();
+  ll_finish();   // before the flagged components' return
   if (stage == kReduceFlagging) {
     const bool bad = bad_sh != 0;
     if (threadIdx.x == 0) {
