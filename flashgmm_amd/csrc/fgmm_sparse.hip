@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kT) void sp_piece_kernel(
       const bool en_ok = en_at < (rn < e1 ? e1 : nxt.y);
       const int2 entr = sorted[en_ok ? en_at : 0];
       const int2 entn = en_ok ? entr : make_int2(0, 0);
-      const float x2r = xm[ent.x];   // a point index (0 past the piece)
+      const float x2r = xm[w < 0.f ? ent.x : 0];   // others read one shared element
       const float x2b = w < 0.f ? x2r : 0.f;
       for (int e = gw; e < nex; e += kWaveRows) {
         int2 en[U];
