@@ -148,6 +148,8 @@ constexpr int kSpCap = 16;            // list entries per point (at most K)
 constexpr int kSpPts = 256;           // points per sort chunk
 constexpr int kSpChunkCap = 2048;     // entries a chunk may hold (more: overflow points)
 constexpr int kSpPiece = 64;          // entries per accumulation piece (at least)
+constexpr int kSpPieceMax = 256;      // ... and at most, unless the piece rows' budget needs more
+constexpr int kSpPieceSpread = 512;   // pieces the length aims for (total entries / this)
 constexpr int kSpFoldRows = 64;       // a component's piece rows beyond this are summed in groups
 
 // Buffers of the sparse Pass 2 (see fgmm_sparse.hip).

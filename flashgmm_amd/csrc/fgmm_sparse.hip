@@ -309,10 +309,15 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
     }
     carry += tot;
   }
-  // piece length: kSpPiece, or more when the piece rows would pass the budget
+  // piece length: about total / kSpPieceSpread entries, at least kSpPiece
+  // and at most kSpPieceMax (one round of the piece kernel: fewer, longer
+  // pieces cost fewer row sums and folds, while enough of them remain to
+  // spread over the chip); more when the piece rows would pass the budget
   // (pieces <= total / piece + Kp <= budget + Kp)
   const long total = carry;
-  int piece = kSpPiece;
+  long pl = total / kSpPieceSpread;
+  pl = pl < kSpPiece ? kSpPiece : (pl > kSpPieceMax ? kSpPieceMax : pl);
+  int piece = (int)pl;
   if ((total + piece - 1) / piece > budget) piece = (int)((total + budget - 1) / budget);
   int pcarry = 0;
 #pragma unroll
