@@ -557,10 +557,10 @@ def test_sparse_partial_overflow_and_repeatability(cuda):
 
 
 def test_sparse_component_with_folded_pieces(cuda):
-    """One component holds 60000 of 65536 points: its list entries fill ~940
-    accumulation pieces of 64, more than the 64 piece rows a component's
-    reduction reads one by one, so its rows are summed in groups first (the
-    group fold).  The other 127 components sit far apart with ~44 points
+    """One component holds 60000 of 65536 points: its list entries fill ~470
+    accumulation pieces of 128 (the length is the entry total / 512), more
+    than the 64 piece rows a component's reduction reads one by one, so its
+    rows are summed in groups first (the group fold).  The other 127 components sit far apart with ~44 points
     each.  Against the fp64 oracle, and two calls agree bit for bit."""
     import torch
     from flashgmm_amd import flash_gmm_native as C
@@ -636,7 +636,8 @@ def test_sparse_chunk_capacity_cut(cuda):
     a = C.flash_em_fused(*t, variant="sparse")
     torch.cuda.synchronize()
     lib = _lib.load()
-    wsb = lib.fgmm_workspace_bytes(N, K, d, 5)
+    # the fused call's workspace (the cache returns the buffer it used)
+    wsb = lib.fgmm_em_fused_workspace_bytes(N, K, d, 5)
     ws = _lib.workspace(cuda, wsb)
     counts = {}
     for name in ("pcnt", "nov"):
@@ -649,6 +650,46 @@ def test_sparse_chunk_capacity_cut(cuda):
     out = [o.cpu().numpy() for o in a]
     check_ln(out[3], ref[3], "chunk cut")
     check_params(out[:3], ref[:3], "chunk cut")
+    b = C.flash_em_fused(*t, variant="sparse")
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_sparse_pieces_of_several_rounds(cuda):
+    """16 nearly identical components: every point lists all 16 pairs, so
+    each 256-point sort chunk keeps its first 2048 entries (its other points
+    take the dense pass), and the ~2M kept entries over the 4096-row piece
+    budget make pieces of 512 entries, which the piece kernel sums in two
+    rounds of 256; each component's 256 pieces also pass through the group
+    fold.  The workspace's piece length proves the long pieces.  Against the
+    fp64 oracle, and two calls agree bit for bit."""
+    import ctypes
+    import torch
+    from flashgmm_amd import _lib
+    from flashgmm_amd import flash_gmm_native as C
+    rng = np.random.default_rng(33)
+    N, K, d = 262144, 16, 8
+    X = rng.normal(0, 1, (N, d)).astype(np.float32)
+    mu = rng.normal(0, 0.02, (K, d)).astype(np.float32)
+    var = rng.uniform(0.9, 1.1, (K, d)).astype(np.float32)
+    lp = np.full(K, -np.log(K), np.float32)
+    ref = O.c_em_fused(X, mu, var, lp)
+    t = to_dev(cuda, X, mu, var, lp)
+    print("[case] sparse pieces of several rounds", flush=True)
+    a = C.flash_em_fused(*t, variant="sparse")
+    torch.cuda.synchronize()
+    lib = _lib.load()
+    # the fused call's workspace (the cache returns the buffer it used)
+    wsb = lib.fgmm_em_fused_workspace_bytes(N, K, d, 5)
+    ws = _lib.workspace(cuda, wsb)
+    off, nb = ctypes.c_size_t(), ctypes.c_size_t()
+    _lib.check(lib.fgmm_workspace_region(N, K, d, 5, b"nov", ctypes.byref(off), ctypes.byref(nb)))
+    nov = ws[off.value:off.value + nb.value].view(torch.int32).cpu().numpy()
+    assert nov[0] > 0, "no point was cut by the chunk capacity"
+    assert nov[2] > 256, f"pieces of {nov[2]} entries: one round each"
+    out = [o.cpu().numpy() for o in a]
+    check_ln(out[3], ref[3], "pieces of several rounds")
+    check_params(out[:3], ref[:3], "pieces of several rounds")
     b = C.flash_em_fused(*t, variant="sparse")
     for x, y in zip(a, b):
         assert torch.equal(x, y)
