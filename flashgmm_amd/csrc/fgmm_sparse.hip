@@ -49,6 +49,7 @@ constexpr int kTopLen = 8;         // run lengths per thread of the top-level sc
 constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
+static_assert(kSpCap >= 2, "the chunk sort requests two entries with the count");
 constexpr int kPre = kSpCap;       // list entries per point requested ahead in the chunk sort:
                                    // all of them, so a long list costs no extra round trips
 constexpr int kSpCountMax = 2048;  // up to this Kp the chunk sort is a counting sort
@@ -110,23 +111,36 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
     ep_sh = 0;
   }
   // one point per thread; its log-normalizer and its entries (at most
-  // C <= kPre) are requested before the scan (i < m <= C: in bounds)
+  // C <= kPre) are requested before the scan (i < m <= C: in bounds).  The
+  // first two entries (most points list no more) are requested with the
+  // count, at a valid index whatever the count, so that they need no round
+  // trip of their own; the rest once the count is known.
   const long n = p0 + tid;
+  const long nc = n < N ? n : 0;
   int m = 0, ov = 0;
   double s1 = 0.0, l2 = 0.0;
   int kpre[kPre];
   double vpre[kPre];
+  const int c = pcnt[nc];
+  const float xr = xm[nc];
+  const double lr = ln2[nc];
+  const size_t i1 = C > 1 ? (size_t)N + nc : (size_t)nc;   // slot 1 exists when C > 1
+  const int k0 = pk[nc], k1 = pk[i1];
+  const double v0 = pv[nc], v1 = pv[i1];
   if (n < N) {
-    const int c = pcnt[n];
-    s1 = (double)xm[n];
-    l2 = ln2[n];
+    s1 = (double)xr;
+    l2 = lr;
     if (c > C) ov = 1;
     else m = c;
+  }
+  kpre[0] = m > 0 ? k0 : 0;
+  vpre[0] = m > 0 ? v0 : 0.0;
+  kpre[1] = m > 1 ? k1 : 0;
+  vpre[1] = m > 1 ? v1 : 0.0;
 #pragma unroll
-    for (int i = 0; i < kPre; i++) {
-      kpre[i] = i < m ? (int)pk[(size_t)i * N + n] : 0;
-      vpre[i] = i < m ? pv[(size_t)i * N + n] : 0.0;
-    }
+  for (int i = 2; i < kPre; i++) {
+    kpre[i] = i < m ? (int)pk[(size_t)i * N + n] : 0;
+    vpre[i] = i < m ? pv[(size_t)i * N + n] : 0.0;
   }
   const int pos = block_excl_scan<kT>(m, sh, nullptr);
   // entries of the kept points -> LDS keys (component, point) and gamma.
