@@ -253,38 +253,43 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// scans: each component's chunk counts (one wavefront per component) ->
+// scans: each component's chunk counts (one workgroup per component) ->
 // offsets within its run; then the runs, pieces and overflow offsets
 // ---------------------------------------------------------------------------
+// one workgroup per component: its chunk counts, kRowPer consecutive ones
+// per thread, all requested at once (clamped indices, values selected),
+// scanned in the thread and across the workgroup
+constexpr int kRowPer = 16;
 __global__ __launch_bounds__(kT) void sp_rowscan_kernel(int Kp, int nchunk, int* __restrict__ cnt,
                                                         int* __restrict__ rowtot) {
-  const int lane = threadIdx.x & 63;
-  const int k = blockIdx.x * (kT / 64) + (threadIdx.x >> 6);
-  if (k >= Kp) return;
+  __shared__ int sh[kT];
+  const int k = blockIdx.x, tid = threadIdx.x;
   int* row = cnt + (size_t)k * nchunk;
   int carry = 0;
-  constexpr int kB = 8;   // 64-chunk steps whose counts are loaded before they are scanned
-  for (int b0 = 0; b0 < nchunk; b0 += 64 * kB) {
-    int v[kB];
+  for (int b0 = 0; b0 < nchunk; b0 += kT * kRowPer) {
+    const int i0 = b0 + tid * kRowPer;
+    int v[kRowPer];
 #pragma unroll
-    for (int u = 0; u < kB; u++) {
-      const int i = b0 + 64 * u + lane;
-      v[u] = i < nchunk ? row[i] : 0;
+    for (int u = 0; u < kRowPer; u++) {
+      const int i = i0 + u;
+      const int x = row[i < nchunk ? i : 0];
+      v[u] = i < nchunk ? x : 0;
     }
+    int t = 0;
 #pragma unroll
-    for (int u = 0; u < kB; u++) {
-      const int i = b0 + 64 * u + lane;
-      int x = v[u];
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(x, off, 64);
-        if (lane >= off) x += t;
-      }
-      if (i < nchunk) row[i] = carry + x - v[u];
-      carry += __shfl(x, 63, 64);
+    for (int u = 0; u < kRowPer; u++) {   // exclusive within the thread
+      const int x = v[u];
+      v[u] = t;
+      t += x;
     }
+    int tot;
+    const int ex = block_excl_scan<kT>(t, sh, &tot);
+#pragma unroll
+    for (int u = 0; u < kRowPer; u++)
+      if (i0 + u < nchunk) row[i0 + u] = carry + ex + v[u];
+    carry += tot;
   }
-  if (lane == 0) rowtot[k] = carry;
+  if (tid == 0) rowtot[k] = carry;
 }
 
 __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
@@ -714,7 +719,7 @@ hipError_t launch_pass2_sparse(const Geom& g, const float* X, const X32Ws& w, co
                      sp.fcap, sp.cnt, sp.ocnt, sp.xsum);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sp_rowscan_kernel, dim3((g.Kp + kT / 64 - 1) / (kT / 64)), dim3(kT), 0, s,
+  hipLaunchKernelGGL(sp_rowscan_kernel, dim3(g.Kp), dim3(kT), 0, s,
                      g.Kp, g.sp_nchunk, sp.cnt, sp.rowtot);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(sp_top_kernel, dim3(1), dim3(kScanThreads), 2 * sizeof(int) * (g.Kp + 1), s,
