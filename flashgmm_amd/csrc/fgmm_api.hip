@@ -88,7 +88,8 @@ Geom make_geom(long N, int K, int d, int variant) {
   if (g.variant == kMfma || g.variant == kX32 || both_sets(g.variant)) {
     g.dp = round_up(d, 16);
     g.Kp = round_up(K, 32);
-    const int P1 = g.variant == kMfma ? 128 : 16 * x1_waves(g.variant, g.Kp);   // Pass-1 points per workgroup
+    // Pass-1 points per workgroup
+    const int P1 = g.variant == kMfma ? 128 : 16 * x1_waves(g.variant, g.Kp);
     g.p1_blocks = (int)((N + P1 - 1) / P1);
     g.p2_kblocks = (g.Kp / 16 + 3) / 4;   // Pass-2 workgroup: 4 x 16 components
   } else {

@@ -24,8 +24,9 @@
 //                     bitonic beyond; counts per component
 //   sp_rowscan_kernel per component, exclusive scan of its chunk counts
 //   sp_top_kernel     runs (each component's entries become one contiguous
-//                     run ordered by point), accumulation pieces of >= 64
-//                     entries, overflow offsets, bound terms
+//                     run ordered by point), accumulation pieces of 64 to
+//                     256 entries (total / 512; more if the rows' budget
+//                     needs it), overflow offsets, bound terms
 //   sp_place_kernel   moves each chunk's sorted entries to their place;
 //                     copies the overflow points out
 //   sp_piece_kernel   fp64 sums over one piece per workgroup
@@ -463,8 +464,9 @@ __global__ __launch_bounds__(kT) void sp_place_kernel(
 // piece sums.  A piece's entries are taken 256 at a time, one per thread
 // (entry 4 * lane + wavefront of the round, so that a short piece still
 // spreads over the four wavefronts): a bound entry adds its weight times
-// {1, max|x|, max x^2} to the thread's error sums; each wavefront compacts its exact entries, in entry order,
-// into its own LDS slice (ballot and lane counts: no barrier) and gathers
+// {1, max|x|, max x^2} to the thread's error sums; each wavefront compacts
+// its exact entries, in entry order, into its own LDS slice (ballot and
+// lane counts: no barrier) and gathers
 // their rows of X with lane groups of L lanes per row (lane j holds
 // features 4j..4j+3), GW = 64/L rows side by side, 16 rows per batch, so
 // that lanes are spent only on rows that exist.  One barrier per piece, for
