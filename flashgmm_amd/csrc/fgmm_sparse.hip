@@ -47,6 +47,7 @@ namespace {
 constexpr int kT = 256;            // threads of the chunk, scan-tile and piece kernels
 constexpr int kScanThreads = 1024;
 constexpr int kTopLen = 8;         // run lengths per thread of the top-level scan (Kp <= 8192)
+constexpr int kTopChunks = 4;      // chunk values per thread it requests up front
 constexpr int kPointBits = 8;      // point index within a chunk in a sort key
 static_assert((1 << kPointBits) == kSpPts, "sort key layout");
 static_assert(kSpPts == kT, "one point per thread");
@@ -314,8 +315,14 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
     const int v = rowtot[k < Kp ? k : 0];
     lens[u] = k < Kp ? v : 0;
   }
-  const int oc0r = ocnt[tid < nchunk ? tid : 0];
-  const double xs0r = xsum[tid < nchunk ? tid : 0];
+  int ocr[kTopChunks];      // the first kTopChunks x 1024 chunks' overflow counts
+  double xsr[kTopChunks];   // ... and max x^2
+#pragma unroll
+  for (int u = 0; u < kTopChunks; u++) {
+    const int i = u * kScanThreads + tid;
+    ocr[u] = ocnt[i < nchunk ? i : 0];
+    xsr[u] = xsum[i < nchunk ? i : 0];
+  }
   int carry = 0;
 #pragma unroll
   for (int u = 0; u < kTopLen; u++) {
@@ -382,17 +389,29 @@ __global__ __launch_bounds__(kScanThreads) void sp_top_kernel(
                           (G > 1 && i % G == 0) ? min(G, np - i) : 0, lo);
   }
   carry = 0;
-  for (int b = 0; b < nchunk; b += kScanThreads) {
+#pragma unroll
+  for (int u = 0; u < kTopChunks; u++) {   // the preloaded chunks
+    const int b = u * kScanThreads;
+    if (b >= nchunk) break;
     const int i = b + tid;
-    const int v = b == 0 ? (i < nchunk ? oc0r : 0) : (i < nchunk ? ocnt[i] : 0);
+    int tot;
+    const int ex = block_excl_scan<kScanThreads>(i < nchunk ? ocr[u] : 0, sh, &tot);
+    if (i < nchunk) ocnt[i] = carry + ex;
+    carry += tot;
+  }
+  for (int b = kTopChunks * kScanThreads; b < nchunk; b += kScanThreads) {
+    const int i = b + tid;
+    const int v = i < nchunk ? ocnt[i] : 0;
     int tot;
     const int ex = block_excl_scan<kScanThreads>(v, sh, &tot);
     if (i < nchunk) ocnt[i] = carry + ex;
     carry += tot;
   }
   if (tid == 0) nov[0] = carry;
-  double a = tid < nchunk ? xs0r : 0.0;
-  for (int i = tid + kScanThreads; i < nchunk; i += kScanThreads) a = fmax(a, xsum[i]);
+  double a = 0.0;
+#pragma unroll
+  for (int u = 0; u < kTopChunks; u++) a = fmax(a, u * kScanThreads + tid < nchunk ? xsr[u] : 0.0);
+  for (int i = kTopChunks * kScanThreads + tid; i < nchunk; i += kScanThreads) a = fmax(a, xsum[i]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) a = fmax(a, __shfl_xor(a, off, 64));
   if ((tid & 63) == 0) d1[tid >> 6] = a;
