@@ -49,7 +49,10 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // few workgroups and its merge of their partial rows stays small.
 static bool small_fits(long N, int K, int d) {
   if (K > kSmallMaxK || d > kSmallMaxD || N > 16384) return false;
-  const long G = (N + small_points(K, d) - 1) / small_points(K, d);
+  // the scope set with 256-point workgroups (128 where their LDS would not
+  // fit) and a one-level merge, kept for the 64-point, two-level kernel
+  const int P0 = small_lds_bytes(K, d, 256) <= kSmallMaxLds ? 256 : 128;
+  const long G = (N + P0 - 1) / P0;
   return G * K * (2L * d + 1) <= 65536;
 }
 
@@ -210,7 +213,9 @@ WsLayout make_layout(const Geom& g) {
     L.aux = 0;
     L.lnsum = 256;
     L.part = align256(L.lnsum + sizeof(double) * (size_t)g.p1_blocks);
-    L.total = align256(L.part + sizeof(double) * (size_t)g.p2_chunks * g.K * g.stat_w);
+    L.grow = align256(L.part + sizeof(double) * (size_t)g.p2_chunks * g.K * g.stat_w);
+    L.total = align256(L.grow + sizeof(double) * (size_t)small_groups(g.p1_blocks) * g.K *
+                                    g.stat_w);
     L.params = L.bias = L.ln2 = L.total;
     return L;
   }
@@ -301,9 +306,10 @@ static int validate_shape(long N, int K, int d, int variant) {
     return fail(FGMM_EINVAL, "d must be in [1, %d] (got %d)", kMaxD, d);
   if (variant < 0 || variant > kLastVariant)
     return fail(FGMM_EINVAL, "unknown variant %d", variant);
-  if (variant == kSmall && (K > kSmallMaxK || d > kSmallMaxD))
-    return fail(FGMM_EINVAL, "the small variant supports K <= %d and d <= %d (got K=%d, d=%d)",
-                kSmallMaxK, kSmallMaxD, K, d);
+  if (variant == kSmall && (K > kSmallMaxK || d > kSmallMaxD || N > kSmallMaxN))
+    return fail(FGMM_EINVAL,
+                "the small variant supports K <= %d, d <= %d and N <= %ld (got K=%d, d=%d, N=%ld)",
+                kSmallMaxK, kSmallMaxD, kSmallMaxN, K, d, N);
   if (variant == kSparse && (d > 128 || K > 8192))
     return fail(FGMM_EINVAL, "the sparse variant supports d <= 128 and K <= 8192 (got d=%d, K=%d)",
                 d, K);
@@ -388,13 +394,20 @@ static Ws carve(const Geom& g, void* ws, const WsLayout& L) {
 static unsigned* small_counter(void* ws, const WsLayout& L) {
   return reinterpret_cast<unsigned*>(static_cast<char*>(ws) + L.aux);
 }
-static int run_small(const Geom& g, const float* X, Ws& w, unsigned* counter,
+static double* small_grow(void* ws, const WsLayout& L) {
+  return reinterpret_cast<double*>(static_cast<char*>(ws) + L.grow);
+}
+static int small_reset(const Geom& g, void* ws, const WsLayout& L, hipStream_t s) {
+  return check_hip(launch_small_reset(small_counter(ws, L), 1 + small_groups(g.p1_blocks), s),
+                   "counter reset");
+}
+static int run_small(const Geom& g, const float* X, Ws& w, unsigned* counter, double* grow,
                      const float* mu_in, const float* var_in, const float* lp_in,
                      float* mu_out, float* var_out, float* lp_out, float* ln_out,
                      double* ll_out, hipStream_t s) {
   Timed t(1, s);
   return check_hip(launch_em_small(g, X, mu_in, var_in, lp_in, mu_out, var_out, lp_out, ln_out,
-                                   w.part, w.lnsum, counter, ll_out, s),
+                                   w.part, w.lnsum, counter, ll_out, grow, s),
                    "fused iteration (small)");
 }
 
@@ -568,10 +581,9 @@ static int em_fused_impl(const float* X, const float* mu, const float* var,
   hipStream_t s = static_cast<hipStream_t>(stream);
   Ws w = carve(g, ws, L);
   if (g.variant == kSmall) {
-    if ((rc = check_hip(launch_small_reset(small_counter(ws, L), s), "counter reset")))
-      return rc;
-    return run_small(g, X, w, small_counter(ws, L), mu, var, log_pi, new_mu, new_var, new_log_pi,
-                     log_normalizer, nullptr, s);
+    if ((rc = small_reset(g, ws, L, s))) return rc;
+    return run_small(g, X, w, small_counter(ws, L), small_grow(ws, L), mu, var, log_pi, new_mu,
+                     new_var, new_log_pi, log_normalizer, nullptr, s);
   }
   if ((rc = run_precompute(g, mu, var, log_pi, w, s))) return rc;
   if ((rc = run_pass1(g, X, w, log_normalizer, s))) return rc;
@@ -800,10 +812,10 @@ int fgmm_em_fit(const float* X, const float* mu0, const float* var0, const float
   Ws w = carve(g, ws, L);
   if (g.variant == kSmall) {   // one launch per iteration, parameters in the outputs
     unsigned* ctr = small_counter(ws, L);
-    if ((rc = check_hip(launch_small_reset(ctr, s), "counter reset"))) return rc;
+    if ((rc = small_reset(g, ws, L, s))) return rc;
     for (int it = 0; it < iters; it++) {
       const bool first = it == 0;
-      rc = run_small(g, X, w, ctr, first ? mu0 : mu_out, first ? var0 : var_out,
+      rc = run_small(g, X, w, ctr, small_grow(ws, L), first ? mu0 : mu_out, first ? var0 : var_out,
                      first ? log_pi0 : log_pi_out, mu_out, var_out, log_pi_out, nullptr,
                      ll_traj + it, s);
       if (rc) return rc;

@@ -41,10 +41,16 @@ constexpr int kSmallMaxD = 64;
 constexpr size_t kSmallMaxLds = 159 * 1024;   // gfx950: 160 KiB of LDS per workgroup, less static
 // LDS of one small-variant workgroup of P points (fgmm_small.hip).
 size_t small_lds_bytes(int K, int d, int P);
-// Points per small-variant workgroup: 256, or 128 when 256 would not fit.
-inline int small_points(int K, int d) {
-  return small_lds_bytes(K, d, 256) <= kSmallMaxLds ? 256 : 128;
-}
+// Points per small-variant workgroup: 64 (a wavefront's width; more, shorter
+// workgroups, whose partial rows the two-level merge absorbs).
+inline int small_points(int, int) { return 64; }
+// Workgroups merged per first-level group, and the arrival counters (one for
+// the groups, one per group) that the workspace's first 256 bytes hold.
+constexpr int kSmallGroup = 8;
+constexpr int kSmallCounters = 64;
+// largest N the small variant takes when forced: its counters fill 256 bytes
+constexpr long kSmallMaxN = 64L * kSmallGroup * (kSmallCounters - 1);
+inline int small_groups(long G) { return (int)((G + kSmallGroup - 1) / kSmallGroup); }
 // Variants that keep both the fp64 fragment-ordered coefficient set and the
 // x32 set behind it.
 __host__ __device__ inline bool both_sets(int v) { return v == kMixed || v == kSparse; }
@@ -86,6 +92,7 @@ struct WsLayout {
   size_t part;      // fp64 [S][Kp][stat_w] sufficient-statistic partials
   size_t aux;       // x32 only: fp32 window anchor [N], max x^2 [N], candidate
                     // slots [N][kX32Slots] (u16 component, fp32 gamma), flags [Kp]
+  size_t grow = 0;  // small only: fp64 group rows [small_groups(G)][K][2d+1]
   size_t total;
 };
 
@@ -350,14 +357,17 @@ hipError_t launch_lse_rows(long N, int K, const double* Lmat, float* gamma,
 // Pass-2 partial layout of g (g describes an MFMA geometry; d <= 256).
 hipError_t launch_gamma_stats(const Geom& g, const float* X, const float* gamma,
                               double* part, hipStream_t s);
-// Small variant: one fused iteration per launch (fgmm_small.hip).  `counter`
-// must be 0 before the first launch (launch_small_reset); each launch leaves
-// it 0.  mu_in/var_in/lp_in may alias mu_out/var_out/lp_out.
+// Small variant: one fused iteration per launch (fgmm_small.hip).  The
+// 1 + small_groups(G) counters must be 0 before the first launch
+// (launch_small_reset); each launch leaves them 0.  grow holds the group
+// rows [small_groups(G)][K][2d+1].  mu_in/var_in/lp_in may alias
+// mu_out/var_out/lp_out.
 hipError_t launch_em_small(const Geom& g, const float* X, const float* mu_in,
                            const float* var_in, const float* lp_in, float* mu_out,
                            float* var_out, float* lp_out, float* ln_out, double* part,
-                           double* lnsum, unsigned* counter, double* ll_out, hipStream_t s);
-hipError_t launch_small_reset(unsigned* counter, hipStream_t s);
+                           double* lnsum, unsigned* counter, double* ll_out, double* grow,
+                           hipStream_t s);
+hipError_t launch_small_reset(unsigned* counter, int n, hipStream_t s);
 hipError_t launch_pass1_x32(const Geom& g, const float* X, const X32Ws& w, double* ln2,
                             float* ln_out, double* lnsum, hipStream_t s);
 hipError_t launch_pass2_x32(const Geom& g, const float* X, const X32Ws& w,

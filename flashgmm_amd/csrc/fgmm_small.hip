@@ -2,8 +2,8 @@
 // d <= 64, few workgroups), where the multi-kernel pipeline is bound by
 // launch and dependency latency rather than by work (C1: N=4096, K=8, d=32).
 //
-// Workgroup = 1024 threads over P points (P = 256, or 128 when the LDS of
-// 256 would not fit), T = 1024 / P threads per point.  Per launch:
+// Workgroup = 1024 threads over P = 64 points, T = 1024 / P threads per
+// point (more, shorter workgroups: at C1 64 of them).  Per launch:
 //   1. the component parameters (fp32 mu, var, log_pi, read as given) become
 //      fp64 mu, 1/var and the log-density constant in LDS; the workgroup's
 //      X rows are staged in LDS (row stride d+1);
@@ -16,11 +16,13 @@
 //      both components over its range in point order (fp64), and the Q range
 //      sums are added in range order into the workgroup's partial row
 //      [K][2d+1]; the workgroup's sum of ln too;
-//   4. one device-scope counter (thread 0 fences for the workgroup): the
-//      workgroup that arrives last merges the partial rows in workgroup
-//      order (fp64; the loads of 16 rows are in flight together), runs the M-step with the native clamps, writes the
-//      fp32 parameters (the next launch's input) and the mean log-normalizer,
-//      and resets the counter.
+//   4. a two-level merge behind device-scope counters (thread 0 fences for
+//      the workgroup): the last of each group of 8 workgroups to arrive sums
+//      their partial rows in workgroup order into a group row; the last
+//      group to finish sums the group rows in group order (fp64; 16 rows'
+//      loads in flight together), runs the M-step with the native clamps,
+//      writes the fp32 parameters (the next launch's input) and the mean
+//      log-normalizer; the last arrivals reset the counters.
 // Every sum runs in a fixed order: results are bitwise repeatable.
 //
 // Reference kernels this fuses (file:line in the reference repository):
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(kThr) void em_small_kernel(
     const float* __restrict__ X, long N, int K, int d, int P, const float* mu_in,
     const float* var_in, const float* lp_in, float* mu_out, float* var_out, float* lp_out,
     float* __restrict__ ln_out, double* __restrict__ part, double* __restrict__ lnsum,
-    unsigned* __restrict__ counter, double* __restrict__ ll_out) {
+    unsigned* __restrict__ counter, double* __restrict__ ll_out, double* __restrict__ grow) {
   extern __shared__ double smem[];
   double* s_mu = smem;
   double* s_iv = s_mu + (size_t)K * d;
@@ -196,39 +198,72 @@ __global__ __launch_bounds__(kThr) void em_small_kernel(
     lnsum[blockIdx.x] = t;
   }
 
-  // 4. the last workgroup to arrive merges the partials and runs the M-step
-  // Thread 0 alone fences (release before the arrival, acquire after it in
-  // the last workgroup); the workgroup barrier extends both to the other
-  // threads.  A device-scope fence writes back / invalidates the L2, so one
-  // per wave would cost far more than the merge.
+  // 4. the partial rows are merged in two levels: the last workgroup of
+  // each group of kSmallGroup to arrive sums its group's rows (in workgroup
+  // order) into a group row; the last group to finish sums the group rows
+  // (in group order) and runs the M-step.  Thread 0 alone fences (release
+  // before an arrival, acquire after it in the last arrival); the
+  // workgroup barrier extends both to the other threads.  A device-scope
+  // fence writes back / invalidates the L2, so one per wave would cost far
+  // more than the merge.  counter[0] counts finished groups, counter[1 + g]
+  // the arrivals of group g; the last arrivals reset them for the next
+  // launch (stream order).
+  const int grp = blockIdx.x / kSmallGroup, ngroups = (G + kSmallGroup - 1) / kSmallGroup;
+  const int gw0 = grp * kSmallGroup;
+  const int gsz = G - gw0 < kSmallGroup ? G - gw0 : kSmallGroup;
   __syncthreads();
   if (tid == 0) {
     __threadfence();
-    const bool l = atomicAdd(counter, 1u) == (unsigned)(G - 1);
+    const bool l = atomicAdd(counter + 1 + grp, 1u) == (unsigned)(gsz - 1);
     if (l) __threadfence();
     last = l;
   }
   __syncthreads();
   if (!last) return;
-  // item (k, j) per thread; its partial rows are loaded kAhead at a time,
-  // all loads of a group in flight together, and summed in workgroup order
+  {
+    const int KW = K * W;
+    double* gr = grow + (size_t)grp * KW;
+    for (int c = tid; c < KW; c += kThr) {
+      double v[kSmallGroup];
+#pragma unroll
+      for (int u = 0; u < kSmallGroup; u++)
+        v[u] = part[(size_t)(gw0 + (u < gsz ? u : 0)) * KW + c];
+      double a = 0.0;
+#pragma unroll
+      for (int u = 0; u < kSmallGroup; u++)
+        if (u < gsz) a += v[u];
+      gr[c] = a;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    counter[1 + grp] = 0u;
+    __threadfence();
+    const bool l = atomicAdd(counter, 1u) == (unsigned)(ngroups - 1);
+    if (l) __threadfence();
+    last = l;
+  }
+  __syncthreads();
+  if (!last) return;
+  // item (k, j) per thread; its group rows are loaded kAhead at a time,
+  // all loads of a batch in flight together, and summed in group order
   constexpr int kAhead = 16;
   for (int it = tid; it < K * d; it += kThr) {
     const int k = it / d, j = it - k * d;
     double nk = 0.0, s = 0.0, q = 0.0;
-    for (int g0 = 0; g0 < G; g0 += kAhead) {
+    for (int g0 = 0; g0 < ngroups; g0 += kAhead) {
       double a[kAhead], b[kAhead], c[kAhead];
 #pragma unroll
       for (int u = 0; u < kAhead; u++) {
-        const int g = g0 + u < G ? g0 + u : G - 1;
-        const double* rr = part + ((size_t)g * K + k) * W;
+        const int g = g0 + u < ngroups ? g0 + u : ngroups - 1;
+        const double* rr = grow + ((size_t)g * K + k) * W;
         a[u] = rr[0];
         b[u] = rr[1 + j];
         c[u] = rr[1 + d + j];
       }
 #pragma unroll
       for (int u = 0; u < kAhead; u++) {
-        if (g0 + u < G) {
+        if (g0 + u < ngroups) {
           nk += a[u];
           s += b[u];
           q += c[u];
@@ -265,25 +300,28 @@ __global__ __launch_bounds__(kThr) void em_small_kernel(
   if (tid == 0) *counter = 0u;   // ready for the next launch (stream order)
 }
 
-__global__ void zero_u32_kernel(unsigned* p, int n) {
+__global__ void zero_u32_kernel(unsigned* p, int n) {   // n <= blockDim
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
 }
 
 }  // namespace
 
-hipError_t launch_small_reset(unsigned* counter, hipStream_t s) {
-  hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, s, counter, 1);
+hipError_t launch_small_reset(unsigned* counter, int n, hipStream_t s) {
+  if (n < 1 || n > 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, s, counter, n);
   return hipGetLastError();
 }
 
 hipError_t launch_em_small(const Geom& g, const float* X, const float* mu_in,
                            const float* var_in, const float* lp_in, float* mu_out,
                            float* var_out, float* lp_out, float* ln_out, double* part,
-                           double* lnsum, unsigned* counter, double* ll_out, hipStream_t s) {
+                           double* lnsum, unsigned* counter, double* ll_out, double* grow,
+                           hipStream_t s) {
   static bool attr_set = false;
   const int P = (int)g.p2_chunk;
-  if (P * (kThr / P) != kThr || P > kThr) return hipErrorInvalidValue;
+  if (P * (kThr / P) != kThr || P > kThr || P % 64 != 0) return hipErrorInvalidValue;
+  if (1 + small_groups(g.p1_blocks) > kSmallCounters || grow == nullptr) return hipErrorInvalidValue;
   const size_t lds = small_lds_bytes(g.K, g.d, P);
   if (lds > kSmallMaxLds) return hipErrorInvalidValue;
   if (!attr_set) {
@@ -295,7 +333,7 @@ hipError_t launch_em_small(const Geom& g, const float* X, const float* mu_in,
   }
   hipLaunchKernelGGL(em_small_kernel, dim3(g.p1_blocks), dim3(kThr), lds, s, X, g.N, g.K, g.d,
                      P, mu_in, var_in, lp_in, mu_out, var_out, lp_out, ln_out, part, lnsum,
-                     counter, ll_out);
+                     counter, ll_out, grow);
   return hipGetLastError();
 }
 
