@@ -30,8 +30,9 @@
  * log-normalizer pass with the fp64 statistics pass) or FGMM_VARIANT_SPARSE
  * (the x32 log-normalizer pass listing each point's significant pairs, and a
  * statistics pass over those lists) or FGMM_VARIANT_SMALL (every stage of an
- * iteration in one launch, fp64; K <= 32, d <= 64; AUTO picks it for
- * N <= 16384 when the merge of its per-workgroup rows stays small) force one.
+ * iteration in one launch, fp64; K <= 32, d <= 64, N <= 32256; AUTO picks
+ * it for N <= 16384 when the merge of its per-workgroup rows stays small)
+ * force one.
  */
 #ifndef FLASHGMM_H
 #define FLASHGMM_H
@@ -53,7 +54,7 @@ extern "C" {
 #define FGMM_VARIANT_X32 3   /* fp32 matrix-core distance + exact fp64 refinement */
 #define FGMM_VARIANT_MIXED 4 /* x32 Pass 1 (exact log-normalizer) + fp64 MFMA Pass 2 */
 #define FGMM_VARIANT_SPARSE 5 /* x32 Pass 1 + statistics from the listed exact pairs */
-#define FGMM_VARIANT_SMALL 6  /* one launch per iteration (K <= 32, d <= 64) */
+#define FGMM_VARIANT_SMALL 6  /* one launch per iteration (K <= 32, d <= 64, N <= 32256) */
 
 /* Library ABI version (major*100 + minor). */
 int fgmm_version(void);

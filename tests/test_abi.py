@@ -147,6 +147,7 @@ def test_argument_errors_before_device_work(lib):
     assert _em(lib, K=8193, variant=5) == 1 and b"sparse" in lib.fgmm_last_error()
     assert _em(lib, K=33, variant=6) == 1 and b"small" in lib.fgmm_last_error()
     assert _em(lib, d=65, variant=6) == 1 and b"small" in lib.fgmm_last_error()
+    assert _em(lib, N=32257, variant=6) == 1 and b"small" in lib.fgmm_last_error()
     for i in range(8):
         assert _em(lib, null=i) == 1 and b"must not be NULL" in lib.fgmm_last_error()
     assert _em(lib, ws=None) == 2 and b"NULL" in lib.fgmm_last_error()
