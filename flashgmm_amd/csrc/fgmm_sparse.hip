@@ -149,9 +149,9 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
   // Offsets come from the uncut prefix, so the points whose entries would
   // pass the chunk capacity form a suffix of the chunk; they join the
   // overflow points and the kept entries fill [0, Ek).
-  int mine = 0;
+  int mine = 0, cutme = INT_MAX, epme = 0;
   if (m > 0 && pos + m > kSpChunkCap) {
-    atomicMin(&cut_sh, tid);
+    cutme = tid;
     ov = 1;
   } else if (m > 0) {
     auto put = [&](int i, int kb, double v) {
@@ -170,10 +170,24 @@ __global__ __launch_bounds__(kT) void sp_sort_kernel(
 #pragma unroll
     for (int i = 0; i < kPre; i++)
       if (i < m) put(i, kpre[i], vpre[i]);
-    atomicMax(&ep_sh, pos + m);
+    epme = pos + m;
   }
-  atomicAdd(&ov_sh, ov);
-  atomicAdd(&ek_sh, mine);
+  // the chunk's cut, overflow count, kept entries and positions written:
+  // reduced over the wavefront by shuffles, one LDS atomic per wavefront
+  // (256 same-address atomics serialise: they took a third of the kernel)
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    cutme = min(cutme, __shfl_xor(cutme, off, 64));
+    epme = max(epme, __shfl_xor(epme, off, 64));
+    ov += __shfl_xor(ov, off, 64);
+    mine += __shfl_xor(mine, off, 64);
+  }
+  if ((tid & 63) == 0) {
+    if (cutme != INT_MAX) atomicMin(&cut_sh, cutme);
+    if (epme > 0) atomicMax(&ep_sh, epme);
+    if (ov > 0) atomicAdd(&ov_sh, ov);
+    if (mine > 0) atomicAdd(&ek_sh, mine);
+  }
   __syncthreads();
   const int cut = cut_sh;
   const int Ek = ek_sh;    // kept entries; after the sort they lead
