@@ -266,7 +266,9 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
   // (the last item again once the queue is spent, its result unused), finds
   // the owning point p by binary search over the inclusive prefix counts,
   // reads the component from p's list and p's features from lane (g, p) of
-  // its own row; two shuffles complete the distance.  The value goes back
+  // its own row (XL_: from the wavefront's LDS copy of its points' features,
+  // as the final evaluation has them); two shuffles complete the distance.
+  // The value goes back
   // into the list slot it came from, and every lane then folds its own
   // entries in list order into its sums.
 #define FGMM_X1_EVAL_QUEUE                                                            \
@@ -305,8 +307,17 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
           const float4 m_ = cm_[4 * w_], v4_ = cv_[4 * w_];                           \
           const float mv_[4] = {m_.x, m_.y, m_.z, m_.w};                              \
           const float vv_[4] = {v4_.x, v4_.y, v4_.z, v4_.w};                          \
+          float xs_[4];                                                               \
+          if constexpr (XL_) {                                                        \
+            const float4 x4_ = reinterpret_cast<const float4*>(xw_)[                  \
+                (g * 16 + p_) * (QX / 4) + (w_ + p_) % (QX / 4)];                     \
+            xs_[0] = x4_.x; xs_[1] = x4_.y; xs_[2] = x4_.z; xs_[3] = x4_.w;           \
+          } else {                                                                    \
+            _Pragma("unroll") for (int i4_ = 0; i4_ < 4; i4_++)                       \
+                xs_[i4_] = __shfl(xq[4 * w_ + i4_], p_, 16);                          \
+          }                                                                           \
           _Pragma("unroll") for (int i4_ = 0; i4_ < 4; i4_++) {                       \
-            const float xv_ = __shfl(xq[4 * w_ + i4_], p_, 16);                       \
+            const float xv_ = xs_[i4_];                                               \
             const double t_ = (double)xv_ - (double)mv_[i4_];                         \
             q_ = fma(t_ * t_, recip_f64((double)vv_[i4_]), q_);                       \
           }                                                                           \
@@ -542,7 +553,11 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
       }
     }
     if (__ballot(cm != 0) != 0ull) {
-      if (__ballot(npend + __popc(cm) > kPendL) != 0ull) FGMM_X1_FLUSH(thr)
+      if (__ballot(npend + __popc(cm) > kPendL) != 0ull) {
+        constexpr bool XL_ = false;   // the tile buffers are in use: shuffles
+        const float* xw_ = nullptr;
+        FGMM_X1_FLUSH(thr)
+      }
 #pragma unroll
       for (int u = 0; u < 8; u++) {
         if (cm & (1u << u)) {
@@ -566,7 +581,24 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
     for (int w = 0; w < kW1; w++) a += dsh[(ntiles - 1) & 1][w][tid];
     dmass[(size_t)((ntiles - 1) * 16 * kSub1 + tid) * gridDim.x + blockIdx.x] = a * (1.0f + 0x1p-16f);
   }
-  FGMM_X1_FLUSH(Mrun - kWinP1)
+  {
+    // The sweep is over (its last barrier passed), so the tile buffers are
+    // free: each wavefront copies its points' features there, lane (g, c)'s
+    // QX floats as float4 (g 16 + c) (QX/4) + (w + c) mod (QX/4) (rotated by
+    // the point, so the 16 columns of a lane group reading 16 different
+    // points hit different banks), and the evaluation reads them with one
+    // LDS load per four features instead of four shuffles.
+    constexpr bool XL_ = BF;
+    static_assert(!BF || W * 64 * QX <= NBUF * TILE, "feature copies fit the tile buffers");
+    float* xw_ = smemf + wave * (64 * QX);
+    if (BF) {
+#pragma unroll
+      for (int w = 0; w < QX / 4; w++)
+        reinterpret_cast<float4*>(xw_)[(g * 16 + c) * (QX / 4) + (w + c) % (QX / 4)] =
+            make_float4(xq[4 * w], xq[4 * w + 1], xq[4 * w + 2], xq[4 * w + 3]);
+    }
+    FGMM_X1_FLUSH(Mrun - kWinP1)
+  }
 #undef FGMM_X1_FLUSH
 #undef FGMM_X1_EVAL_QUEUE
 
