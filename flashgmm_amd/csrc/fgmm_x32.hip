@@ -68,15 +68,29 @@ constexpr int x1_tile_floats(int dp, int mode) {
 // kSpKeep) = 2^-126)
 constexpr float kSpKeep = 86.0f;
 
-// Sum over the 16 lanes of each DPP row (lanes 16g .. 16g+15); every lane of
-// the row gets the sum.  Quad swaps, then half-row and row mirrors.
-__device__ inline float row16_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
-  return v;
+#define FGMM_DPP(v, ctrl) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, false))
+// Sums of eight values per lane over the 16 lanes of each DPP row (lanes
+// 16g .. 16g+15), reduce-scatter style: lane c of a row ends with the sum of
+// value (c >> 1) & 7 (lanes c and c ^ 1 alike).  Each step pairs a lane with
+// one whose lane bit differs (row mirror: bit 3, half-row mirror: bit 2,
+// quad swap: bit 1); the lane keeps the half of its values that its bit
+// selects, adds the partner's copy of that half and passes on the other.  A
+// final quad swap (bit 0) completes the sums.  22 DPP-fed operations
+// instead of 32 for eight full row sums.
+__device__ inline float row16_scatter8(const float (&v)[8], int c) {
+  const bool b3 = (c & 8) != 0, b2 = (c & 4) != 0, b1 = (c & 2) != 0;
+  float n[4], m[2];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    n[j] = (b3 ? v[4 + j] : v[j]) + FGMM_DPP(b3 ? v[j] : v[4 + j], 0x140);
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+    m[j] = (b2 ? n[2 + j] : n[j]) + FGMM_DPP(b2 ? n[j] : n[2 + j], 0x141);
+  float r = (b1 ? m[1] : m[0]) + FGMM_DPP(b1 ? m[0] : m[1], 0x4E);
+  return r + FGMM_DPP(r, 0xB1);
 }
+#undef FGMM_DPP
 
 __device__ inline f32x4 mfma32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -543,13 +557,12 @@ __global__ __launch_bounds__(64 * W, 2) void pass1_x32_kernel(
         dv[u] = (valid && !(cm & (1u << u))) ? __builtin_amdgcn_exp2f(hi[u] - Mrun) : 0.f;
         any = any || dv[u] > 0.f;
       }
-      if (__ballot(any) != 0ull) {
-#pragma unroll
-        for (int u = 0; u < 8; u++) dv[u] = row16_sum(dv[u]);
-      }
-      if (c == 0) {
-#pragma unroll
-        for (int u = 0; u < 8; u++) dsh[buf][wave][(u >> 2) * 16 + 4 * g + (u & 3)] = dv[u];
+      // lane c of a lane group holds the sum of value (c >> 1); the even
+      // lanes store them, one LDS store for all eight
+      const float dsum = __ballot(any) != 0ull ? row16_scatter8(dv, c) : 0.f;
+      if ((c & 1) == 0) {
+        const int u = c >> 1;
+        dsh[buf][wave][(u >> 2) * 16 + 4 * g + (u & 3)] = dsum;
       }
     }
     if (__ballot(cm != 0) != 0ull) {
